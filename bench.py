@@ -1,0 +1,184 @@
+"""Benchmark of the MeanFlow FM/DiT head on one MI355X.
+
+Workload (one "step" = one full MeanFlow NFE=4 solve over one batch): 64
+concurrent requests, context lengths U{64..1024}, 16 latent rows x 64-d each,
+12-block DiT (hidden 1024, 16 heads x 64, MLP 4096) in bf16, random-init
+weights N(0, 0.02), contexts N(0,1), noise N(0,1), g_cond = 0.
+
+Prints one JSON line:
+  value        DiT GEMM TFLOP/s = 12 * 2*M*(4H^2 + 2HF) * NFE / wall-per-solve,
+               M = sum(c_i + 16) unpadded rows
+  roofline     the dominant kernel (largest total time among the GEMM classes)
+               timed with dispatch-packet HIP events inside the timed region
+  cpu_baseline the oracle's float32 DiT on the host cores over a bounded
+               sample of the same workload (first k requests, full NFE=4 solve)
+
+    python bench.py [--gpus 1] [--steps 10] [--warmup 3]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_BF16_TFLOPS = 2500.0      # MI355X dense bf16 MFMA
+PEAK_HBM_GBS = 8000.0
+FRAME_S = 0.04                 # one latent frame = 1920 samples at 48 kHz
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def cpu_baseline(cfg, W, lens, hist, noise, budget_s: float):
+    """Oracle fp32 MeanFlow solve of the first k requests on the host cores."""
+    import torch
+    from oracle import dit_ref as R
+    threads = min(os.cpu_count() or 1, 16)
+    torch.set_num_threads(threads)
+    k = 1
+    samples = []
+    t_spent = 0.0
+    while True:
+        sub = hist[:k]
+        inp, mask, pos, g = R.pack_fm_inputs(sub, cfg.patch, cfg.hidden)
+        t0 = time.perf_counter()
+        R.meanflow_solve_varlen(W, cfg, sub, g, noise[:k], 4, "fp32")
+        dt = time.perf_counter() - t0
+        t_spent += dt
+        M = sum(L + cfg.patch for L in lens[:k])
+        samples.append((k, M, dt))
+        log(f"cpu baseline: k={k} M={M} {dt:.2f}s")
+        if t_spent + 2.5 * dt > budget_s or k * 2 > len(lens):
+            break
+        k *= 2
+    k, M, dt = samples[-1]
+    flops = R.dit_gemm_flops(cfg, M) * 4
+    return {
+        "value": flops / dt / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
+        "sample": (f"oracle float32 MeanFlow NFE=4 solve of the first {k} of the 64 requests "
+                   f"(M={M} rows/step) on {threads} host threads, torch {torch.__version__}, "
+                   f"mkldnn={torch.backends.mkldnn.is_available()}"),
+        "xRT": k * cfg.patch * FRAME_S / dt,
+        "seconds": dt,
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--requests", type=int, default=64)
+    ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--cpu-budget", type=float, default=20.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: the FM head shards requests across GPUs with no "
+              "collective on the hot path, and this build runs on single-GPU boxes only "
+              "(--gpus 1).", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from oracle import dit_ref as R
+    from nanovllm_dots_amd import FMSpec, HipFMHead, HipMeanflow
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    cfg = R.DitConfig(hidden=1024, heads=16, ffn=4096, n_blocks=12, latent_dim=64, patch=16)
+    log("generating weights / inputs")
+    W = R.random_dit_weights(cfg, args.seed)
+    lens, hist, noise = R.synthetic_requests(args.requests, 64, 1024, cfg, seed=args.seed,
+                                             regime="bf16")
+    inp, _, pos, g = R.pack_fm_inputs(hist, cfg.patch, cfg.hidden)
+    n, T = inp.shape[:2]
+    M = sum(L + cfg.patch for L in lens)
+    head = HipFMHead(FMSpec.of(cfg), W, device=dev)
+    mf = HipMeanflow(None, num_steps=4, dit=object(), head=head)
+    inp_d = inp.to(dev, torch.bfloat16)
+    pos_d = pos.to(dev)
+    g_d = g.to(dev, torch.bfloat16)
+    noise_d = noise.to(dev, torch.bfloat16)
+    del inp
+
+    def solve():
+        return mf(input_sequence=inp_d, attn_mask=None, pos_ids=pos_d, g_cond=g_d, noise=noise_d)
+
+    log(f"warmup x{args.warmup} (n={n}, T={T}, M={M})")
+    for _ in range(args.warmup):
+        out = solve()
+    torch.cuda.synchronize()
+
+    # timed region: K solves; the dominant kernel classes carry dispatch-packet events
+    head.profile(True)
+    head.profile_read()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record()
+    for _ in range(args.steps):
+        out = solve()
+    e1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_total = e0.elapsed_time(e1)
+    prof = head.profile_read()
+    head.profile(False)
+    ms = ms_total / args.steps
+    log(f"timed: {ms:.3f} ms/solve (host wall {wall / args.steps * 1e3:.3f} ms)")
+    assert torch.isfinite(out.float()).all()
+
+    gemm_flops = R.dit_gemm_flops(cfg, M) * 4
+    tflops = gemm_flops / (ms * 1e-3) / 1e12
+    xrt = n * cfg.patch * FRAME_S / (ms * 1e-3)
+    H, F = cfg.hidden, cfg.ffn
+    per_launch = {"qkv_gemm": 2 * M * H * 3 * H, "o_gemm": 2 * M * H * H,
+                  "fc1_gemm": 2 * M * H * F, "fc2_gemm": 2 * M * F * H}
+    classes = {k: v for k, v in prof.items()}
+    dom = max(per_launch, key=lambda k: classes[k][0])
+    dom_ms, dom_n = classes[dom]
+    avg_ms = dom_ms / max(dom_n, 1)
+    achieved = per_launch[dom] / (avg_ms * 1e-3) / 1e12
+    breakdown = {k: {"ms_per_solve": v[0] / args.steps, "launches_per_solve": v[1] / args.steps}
+                 for k, v in classes.items()}
+    gemm_ms = sum(classes[k][0] for k in per_launch) / args.steps
+    log("per-class ms/solve: " + ", ".join(f"{k}={v['ms_per_solve']:.3f}" for k, v in breakdown.items()))
+
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(cfg, W, lens, hist, noise, args.cpu_budget)
+
+    rec = {
+        "metric": "DiT GEMM TFLOPS (% MFMA peak) + latent xRT at 64 streams, NFE=4",
+        "value": round(tflops, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (seeded RandomState; random-init N(0,0.02) weights)",
+        "config": {"workload": "meanflow_nfe4_solve_64req_ctx64-1024", "requests": n,
+                   "ctx_range": [64, 1024], "patch": cfg.patch, "latent_dim": cfg.latent_dim,
+                   "hidden": H, "heads": cfg.heads, "ffn": F, "blocks": cfg.n_blocks, "nfe": 4,
+                   "rotary": cfg.rotary, "qk_norm": cfg.qk_norm, "qkv_bias": cfg.qkv_bias,
+                   "tokens_per_step_unpadded": M, "padded_T": T},
+        "pct_mfma_peak": round(100 * tflops / PEAK_BF16_TFLOPS, 2),
+        "latent_xRT": round(xrt, 1),
+        "gemm_only_tflops": round(gemm_flops / (gemm_ms * 1e-3) / 1e12, 2) if gemm_ms > 0 else None,
+        "roofline": {"bound": "mfma", "kernel": dom, "achieved": round(achieved, 2),
+                     "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": None,
+                     "avg_launch_ms": round(avg_ms, 5), "flops_per_launch": per_launch[dom]},
+        "kernel_breakdown": breakdown,
+        "cpu_baseline": ({k: (round(v, 5) if isinstance(v, float) else v) for k, v in cpu.items()
+                          if k in ("value", "unit", "cores", "kind", "sample")} if cpu else None),
+        "cpu_xRT": round(cpu["xRT"], 4) if cpu else None,
+    }
+    print(json.dumps(rec), flush=True)
+
+
+if __name__ == "__main__":
+    main()

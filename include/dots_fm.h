@@ -1,0 +1,134 @@
+/* dots_fm.h — C ABI of the MI355X (gfx950) MeanFlow FM/DiT head.
+ *
+ * One shared library, libdotsfm.so. Plain C types only: device pointers are
+ * `void*` (memory owned by the caller, e.g. torch tensors), host arrays are
+ * plain pointers, streams are `void*` holding a hipStream_t (NULL = default
+ * stream). Every function returns 0 on success or a nonzero status; the
+ * message of the last failure on the calling thread is dfh_last_error().
+ * No C++ exception crosses this boundary.
+ *
+ * Reference interfaces replaced (paths in the nanovllm_dots repository):
+ *   dfh_meanflow_solve  <- GraphedMeanflow.__call__
+ *                          nanovllm_dots/models/dots/graphed_meanflow.py:36-60, and
+ *                          batched_meanflow nanovllm_dots/models/dots/batched_fm.py:82-126
+ *   dfh_dit_forward     <- DiT.forward (the `vfp` callable)
+ *                          nanovllm_dots/models/dots/native/dit.py:135-148
+ *   dfh_set_weights     <- build_native_dit / load_component weight binding
+ *                          nanovllm_dots/models/dots/native/loader.py:23-67
+ *   dfh_gemm_bf16       <- nn.Linear (cuBLAS bf16 GEMM) as used by the DiT
+ *                          nanovllm_dots/models/dots/native/layers.py:82-84, 152-161
+ *   dfh_quant_act_i8, dfh_quant_weight_i8, dfh_gemm_w8a8
+ *                       <- Int8DynamicLinear nanovllm_dots/models/dots/int8_dit.py:34-65
+ */
+#ifndef DOTS_FM_H
+#define DOTS_FM_H
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct DfhHandle DfhHandle;
+
+/* DiT shape. Mirrors the checkpoint config's DiT block
+ * (nanovllm_dots/models/dots/native/config.py:46-47, loader.py:52-67) and the core
+ * scalars latent_dim / latent_patch_size (native/core.py:50-55).
+ * Supported: head_dim == 64, hidden % 256 == 0, ffn % 256 == 0,
+ * latent_dim % 64 == 0, freq_dim % 64 == 0. */
+typedef struct DfhConfig {
+  int hidden;
+  int heads;
+  int head_dim;
+  int ffn;
+  int n_blocks;
+  int latent_dim;
+  int patch;          /* latent rows per request (latent_patch_size) */
+  int freq_dim;       /* timestep frequency embedding size (256) */
+  int qkv_bias;       /* q/k/v projections carry a bias */
+  int qk_norm;        /* 0 none, 1 LayerNorm(head_dim, affine), 2 RMSNorm(head_dim) */
+  int rotary;         /* RoPE on q and k */
+  int meanflow;       /* duration embedder present (MeanFlow DiT) */
+  float ln_eps;       /* block / final LayerNorm eps (1e-5) */
+  const float* rope_inv_freq;  /* host, head_dim/2 floats (RotaryEmbedding.inv_freq) */
+  const float* temb_freqs;     /* host, freq_dim/2 floats (TimestepEmbedder freqs) */
+} DfhConfig;
+
+/* Device pointers to bf16 parameters in nn.Linear layout ([out, in] row-major),
+ * named after the reference state dict. Optional tensors may be NULL. */
+typedef struct DfhBlockWeights {
+  const void *q_w, *q_b, *k_w, *k_b, *v_w, *v_b;       /* attn.{q,k,v}_proj */
+  const void *q_norm_w, *q_norm_b, *k_norm_w, *k_norm_b; /* attn.{q,k}_norm */
+  const void *o_w, *o_b;                                /* attn.o_proj */
+  const void *fc1_w, *fc1_b, *fc2_w, *fc2_b;            /* ffn.fc1 / ffn.fc2 */
+  const void *ada_w, *ada_b;                            /* adaLN_modulation.1 [6H, H] */
+} DfhBlockWeights;
+
+typedef struct DfhWeights {
+  const void *input_w, *input_b;                 /* input_layer */
+  const void *t_w0, *t_b0, *t_w2, *t_b2;         /* time_embedder.mlp.{0,2} */
+  const void *d_w0, *d_b0, *d_w2, *d_b2;         /* duration_embedder.mlp.{0,2} */
+  const void *final_ada_w, *final_ada_b;         /* output_layer.adaLN_modulation.1 [2H, H] */
+  const void *final_w, *final_b;                 /* output_layer.linear [ld, H] */
+  const void *coord_w, *coord_b;                 /* core.coordinate_proj [H, ld] */
+  const DfhBlockWeights* blocks;                 /* host array of n_blocks */
+} DfhWeights;
+
+/* Whole MeanFlow solve over N padded requests (the input contract of
+ * DotsBatchEngine._pack_fm_inputs, engine.py:635-688). The FM mask is implied
+ * by pos_ids (history length c_i = pos_ids[i, T-P]) and is not read. */
+typedef struct DfhSolveArgs {
+  int n;                    /* requests */
+  int total_len;            /* T = max history + patch */
+  int num_steps;            /* NFE (<= 16) */
+  const void* input_sequence;  /* bf16 [n, T, H], latent slot zero */
+  const void* pos_ids;         /* f32  [n, T] */
+  const void* g_cond;          /* bf16 [n, H] or NULL (zeros) */
+  const void* noise;           /* bf16 [n, P, ld] */
+  void* out;                   /* bf16 [n, P, ld] */
+  const float* t_grid;         /* host [num_steps]: t_s */
+  const float* dt_grid;        /* host [num_steps]: t_{s+1} - t_s */
+} DfhSolveArgs;
+
+/* One DiT forward (the vfp callable) on the padded layout. */
+typedef struct DfhForwardArgs {
+  int n;
+  int total_len;
+  const void* x;            /* bf16 [n, T, H] */
+  const void* timesteps;    /* f32 [n] device */
+  const void* duration;     /* f32 [n] device or NULL */
+  const void* pos_ids;      /* f32 [n, T] */
+  const void* g_cond;       /* bf16 [n, H] or NULL */
+  void* out;                /* bf16 [n, T, ld]; padding rows are written as 0 */
+} DfhForwardArgs;
+
+const char* dfh_last_error(void);
+
+int dfh_create(const DfhConfig* cfg, DfhHandle** out);
+int dfh_destroy(DfhHandle* h);
+/* Packs the weights into handle-owned device memory (fused QKV, one adaLN
+ * matrix for all blocks). Synchronizes the stream. */
+int dfh_set_weights(DfhHandle* h, const DfhWeights* w, void* stream);
+/* Grows the workspace for up to n requests of padded length T and num_steps
+ * solver steps (synchronizes the stream only when it grows). */
+int dfh_reserve(DfhHandle* h, int n, int total_len, int num_steps, void* stream);
+int dfh_meanflow_solve(DfhHandle* h, const DfhSolveArgs* a, void* stream);
+int dfh_dit_forward(DfhHandle* h, const DfhForwardArgs* a, void* stream);
+/* Reads and clears the device-side input check of the last solve/forward
+ * (bit 0: a pos_ids row does not describe a valid FM layout). Synchronizes. */
+int dfh_input_status(DfhHandle* h, int* flags, void* stream);
+
+/* Per-kernel-class timing with dispatch-packet events (bench instrumentation).
+ * classes: 0 qkv gemm, 1 o_proj gemm, 2 fc1 gemm, 3 fc2 gemm, 4 attention,
+ * 5 ln_modulate, 6 other. */
+int dfh_profile_enable(DfhHandle* h, int enable);
+int dfh_profile_read(DfhHandle* h, double* ms_per_class, long* launches_per_class, int n_classes);
+
+/* Standalone bf16 GEMM: C[M,N] = A[M,K] B[N,K]^T + bias (bias may be NULL).
+ * epilogue: 0 bf16 out, 1 GELU(tanh) bf16 out, 4 float32 out. */
+int dfh_gemm_bf16(const void* A, long lda, const void* B, long ldb, void* C, long ldc,
+                  const void* bias, int M, int N, int K, int epilogue, int tile, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DOTS_FM_H */

@@ -1,0 +1,10 @@
+"""nanovllm_dots_amd — the MeanFlow FM/DiT head of nanovllm_dots on MI355X.
+
+Hand-written gfx950 HIP kernels (libdotsfm.so, C ABI in include/dots_fm.h)
+behind the reference's accelerator entry points (``fm_accel="hip"``).
+"""
+from .hip_meanflow import (FMSpec, HipDiT, HipFMHead, HipMeanflow, batched_meanflow,  # noqa: F401
+                           meanflow_grid, rope_inv_freq, timestep_freqs)
+
+__all__ = ["FMSpec", "HipDiT", "HipFMHead", "HipMeanflow", "batched_meanflow", "meanflow_grid",
+           "rope_inv_freq", "timestep_freqs"]

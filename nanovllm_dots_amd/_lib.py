@@ -1,0 +1,112 @@
+"""ctypes binding of libdotsfm.so (include/dots_fm.h).
+
+The library is required: loading fails loudly when it is missing or when no
+GPU is visible. There is no CPU or torch fallback for any entry point.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libdotsfm.so")
+
+vp = C.c_void_p
+
+
+class DfhConfig(C.Structure):
+    _fields_ = [
+        ("hidden", C.c_int), ("heads", C.c_int), ("head_dim", C.c_int), ("ffn", C.c_int),
+        ("n_blocks", C.c_int), ("latent_dim", C.c_int), ("patch", C.c_int), ("freq_dim", C.c_int),
+        ("qkv_bias", C.c_int), ("qk_norm", C.c_int), ("rotary", C.c_int), ("meanflow", C.c_int),
+        ("ln_eps", C.c_float),
+        ("rope_inv_freq", C.POINTER(C.c_float)), ("temb_freqs", C.POINTER(C.c_float)),
+    ]
+
+
+class DfhBlockWeights(C.Structure):
+    _fields_ = [(n, vp) for n in (
+        "q_w", "q_b", "k_w", "k_b", "v_w", "v_b", "q_norm_w", "q_norm_b", "k_norm_w", "k_norm_b",
+        "o_w", "o_b", "fc1_w", "fc1_b", "fc2_w", "fc2_b", "ada_w", "ada_b")]
+
+
+class DfhWeights(C.Structure):
+    _fields_ = [(n, vp) for n in (
+        "input_w", "input_b", "t_w0", "t_b0", "t_w2", "t_b2", "d_w0", "d_b0", "d_w2", "d_b2",
+        "final_ada_w", "final_ada_b", "final_w", "final_b", "coord_w", "coord_b")] + [
+        ("blocks", C.POINTER(DfhBlockWeights))]
+
+
+class DfhSolveArgs(C.Structure):
+    _fields_ = [
+        ("n", C.c_int), ("total_len", C.c_int), ("num_steps", C.c_int),
+        ("input_sequence", vp), ("pos_ids", vp), ("g_cond", vp), ("noise", vp), ("out", vp),
+        ("t_grid", C.POINTER(C.c_float)), ("dt_grid", C.POINTER(C.c_float)),
+    ]
+
+
+class DfhForwardArgs(C.Structure):
+    _fields_ = [
+        ("n", C.c_int), ("total_len", C.c_int), ("x", vp), ("timesteps", vp), ("duration", vp),
+        ("pos_ids", vp), ("g_cond", vp), ("out", vp),
+    ]
+
+
+# exported symbol -> (restype, argtypes); every symbol here is declared in include/dots_fm.h
+SIGNATURES = {
+    "dfh_last_error": (C.c_char_p, []),
+    "dfh_create": (C.c_int, [C.POINTER(DfhConfig), C.POINTER(vp)]),
+    "dfh_destroy": (C.c_int, [vp]),
+    "dfh_set_weights": (C.c_int, [vp, C.POINTER(DfhWeights), vp]),
+    "dfh_reserve": (C.c_int, [vp, C.c_int, C.c_int, C.c_int, vp]),
+    "dfh_meanflow_solve": (C.c_int, [vp, C.POINTER(DfhSolveArgs), vp]),
+    "dfh_dit_forward": (C.c_int, [vp, C.POINTER(DfhForwardArgs), vp]),
+    "dfh_input_status": (C.c_int, [vp, C.POINTER(C.c_int), vp]),
+    "dfh_profile_enable": (C.c_int, [vp, C.c_int]),
+    "dfh_profile_read": (C.c_int, [vp, C.POINTER(C.c_double), C.POINTER(C.c_long), C.c_int]),
+    "dfh_gemm_bf16": (C.c_int, [vp, C.c_long, vp, C.c_long, vp, C.c_long, vp, C.c_int, C.c_int,
+                                C.c_int, C.c_int, C.c_int, vp]),
+}
+
+_lib = None
+
+
+def load_library(path: str = LIB_PATH):
+    """dlopen the library and bind every declared symbol (no GPU needed)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(path):
+        raise RuntimeError(
+            f"libdotsfm.so not found at {path}; build it with `python -m nanovllm_dots_amd.build`")
+    lib = C.CDLL(path)
+    for name, (res, args) in SIGNATURES.items():
+        f = getattr(lib, name)
+        f.restype = res
+        f.argtypes = args
+    _lib = lib
+    return lib
+
+
+def lib():
+    """The library, for a GPU call: raises when no GPU is visible."""
+    import torch
+    if not torch.cuda.is_available():
+        raise RuntimeError("nanovllm_dots_amd needs a ROCm GPU (gfx950); none is visible")
+    return load_library()
+
+
+def check(status: int, what: str = "") -> None:
+    if status != 0:
+        msg = load_library().dfh_last_error().decode(errors="replace")
+        raise RuntimeError(f"{what}: {msg}" if what else msg)
+
+
+def stream_ptr(stream=None):
+    import torch
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return vp(s.cuda_stream)
+
+
+def ptr(t) -> vp:
+    return vp(t.data_ptr()) if t is not None else vp(None)

@@ -1,0 +1,600 @@
+// C ABI of the FM/DiT head: handle, weight packing, workspace and the
+// graph-free MeanFlow launch sequence.
+//
+// The solve (batched_meanflow, nanovllm_dots/models/dots/batched_fm.py:82-126, with
+// DiT.forward, native/dit.py:135-148, as the velocity predictor) is one straight
+// stream-ordered sequence of kernels. Shapes that depend on the request lengths
+// (packed row count M, per-request offsets) are computed on the device from
+// pos_ids; grids are sized from host-known upper bounds (N*T rows) and every
+// kernel reads the device row count, so a new batch shape needs no capture, no
+// host sync and no allocation (once the workspace has grown to it).
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "../../include/dots_fm.h"
+#include "dfh_kernels.h"
+#include "dfh_ops.h"
+
+namespace dfh {
+thread_local LaunchEvents g_launch_events;
+}
+
+using namespace dfh;
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return 1;
+}
+
+#define DFH_CHECK(expr)                                                                   \
+  do {                                                                                    \
+    hipError_t e_ = (expr);                                                               \
+    if (e_ != hipSuccess) return fail("%s failed: %s (%s:%d)", #expr, hipGetErrorString(e_), \
+                                      __FILE__, __LINE__);                                \
+  } while (0)
+
+struct DevBuf {
+  void* p = nullptr;
+  size_t bytes = 0;
+};
+
+hipError_t dev_alloc(DevBuf& b, size_t bytes) {
+  if (b.bytes >= bytes && b.p) return hipSuccess;
+  if (b.p) {
+    hipError_t e = hipFree(b.p);
+    if (e != hipSuccess) return e;
+  }
+  b.p = nullptr;
+  b.bytes = 0;
+  if (bytes == 0) return hipSuccess;
+  hipError_t e = hipMalloc(&b.p, bytes);
+  if (e != hipSuccess) return e;
+  b.bytes = bytes;
+  return hipMemset(b.p, 0, bytes);
+}
+
+template <typename T>
+T* P(DevBuf& b) { return reinterpret_cast<T*>(b.p); }
+
+enum ProfClass { PC_QKV = 0, PC_O, PC_FC1, PC_FC2, PC_ATTN, PC_LN, PC_OTHER, PC_N };
+
+}  // namespace
+
+struct DfhHandle {
+  DfhConfig cfg;
+  std::vector<float> rope_inv_freq, temb_freqs;
+  int ld_mod = 0;  // n_blocks*6H + 2H
+  bool weights_set = false;
+
+  // packed weights (bf16)
+  DevBuf w_arena;
+  const uint16_t *in_w, *in_b, *t_w0, *t_b0, *t_w2, *t_b2, *d_w0, *d_b0, *d_w2, *d_b2;
+  const uint16_t *ada_w, *ada_b, *fin_w, *fin_b, *coord_w, *coord_b;
+  std::vector<const uint16_t*> qkv_w, qkv_b, o_w, o_b, fc1_w, fc1_b, fc2_w, fc2_b;
+  std::vector<const uint16_t*> qn_w, qn_b, kn_w, kn_b;
+  DevBuf consts;  // rope inv_freq, temb freqs (float32)
+
+  // workspace capacity
+  int cap_n = 0, cap_T = 0, cap_S = 0;
+  long cap_M = 0, ld_vt = 0;
+  DevBuf seq, x, hbuf, qk, attn, ff, vt;
+  DevBuf row_req, row_pos, vt_col, cu_rows, cu_vt, hist_len, counts, err, patch_rows;
+  DevBuf rope_cos, rope_sin;
+  DevBuf temb_in, t_hid, t_out, d_hid, d_out, cond, cond_act, mod;
+  DevBuf z, zp, fin, vel, tvals;
+
+  // profiling
+  bool prof = false;
+  std::vector<hipEvent_t> ev_pool;
+  std::vector<std::pair<int, int>> ev_used;  // (class, pool index of start)
+  size_t ev_next = 0;
+  double prof_ms[PC_N] = {0};
+  long prof_n[PC_N] = {0};
+};
+
+namespace {
+
+// arm dispatch-packet events for the next launch of class `pc`
+void prof_arm(DfhHandle* h, int pc) {
+  if (!h->prof) return;
+  if (h->ev_next + 2 > h->ev_pool.size()) return;  // pool full: drop the sample
+  const int i = (int)h->ev_next;
+  h->ev_next += 2;
+  g_launch_events.start = h->ev_pool[i];
+  g_launch_events.stop = h->ev_pool[i + 1];
+  h->ev_used.push_back({pc, i});
+}
+
+int check_cfg(const DfhConfig& c) {
+  if (c.head_dim != 64) return fail("head_dim must be 64 (got %d)", c.head_dim);
+  if (c.heads * c.head_dim != c.hidden) return fail("heads*head_dim != hidden");
+  if (c.hidden % 256 || c.ffn % 256) return fail("hidden and ffn must be multiples of 256");
+  if (c.hidden > 2048) return fail("hidden > 2048 not supported");
+  if (c.latent_dim % 64) return fail("latent_dim must be a multiple of 64");
+  if (c.freq_dim % 64 || c.freq_dim <= 0) return fail("freq_dim must be a positive multiple of 64");
+  if (c.n_blocks <= 0 || c.patch <= 0) return fail("n_blocks and patch must be positive");
+  if (c.qk_norm < 0 || c.qk_norm > 2) return fail("qk_norm must be 0, 1 or 2");
+  if (c.rotary && !c.rope_inv_freq) return fail("rotary requires rope_inv_freq");
+  if (!c.temb_freqs) return fail("temb_freqs is required");
+  return 0;
+}
+
+hipError_t gemm(DfhHandle* h, int pc, const GemmArgs& a, int epi, hipStream_t s, int tile = -1) {
+  prof_arm(h, pc);
+  return gemm_bf16(a, epi, s, tile);
+}
+
+GemmArgs linear_args(const uint16_t* A, long lda, const uint16_t* W, const uint16_t* b, uint16_t* C,
+                     long ldc, int M, const int* M_dev, int N, int K) {
+  GemmArgs a;
+  memset(&a, 0, sizeof(a));
+  a.A = A; a.lda = lda; a.B = W; a.ldb = K; a.C = C; a.ldc = ldc; a.bias = b;
+  a.M = M; a.M_dev = M_dev; a.N = N; a.K = K;
+  return a;
+}
+
+int reserve(DfhHandle* h, int n, int T, int S, hipStream_t s) {
+  const DfhConfig& c = h->cfg;
+  if (n <= h->cap_n && T <= h->cap_T && S <= h->cap_S && (long)n * T <= h->cap_M) return 0;
+  DFH_CHECK(hipStreamSynchronize(s));  // in-flight kernels may still use the old buffers
+  const int nn = n > h->cap_n ? n : h->cap_n;
+  const int TT = T > h->cap_T ? T : h->cap_T;
+  const int SS = S > h->cap_S ? S : h->cap_S;
+  const long M = (long)nn * TT;
+  const long H = c.hidden, F = c.ffn, P = c.patch, ld = c.latent_dim;
+  const long ld_vt = M + 8L * nn + 128;
+  DFH_CHECK(dev_alloc(h->seq, M * H * 2));
+  DFH_CHECK(dev_alloc(h->x, M * H * 2));
+  DFH_CHECK(dev_alloc(h->hbuf, M * H * 2));
+  DFH_CHECK(dev_alloc(h->qk, M * 2 * H * 2));
+  DFH_CHECK(dev_alloc(h->attn, M * H * 2));
+  DFH_CHECK(dev_alloc(h->ff, M * F * 2));
+  DFH_CHECK(dev_alloc(h->vt, (size_t)H * ld_vt * 2));
+  DFH_CHECK(dev_alloc(h->row_req, M * 4));
+  DFH_CHECK(dev_alloc(h->row_pos, M * 4));
+  DFH_CHECK(dev_alloc(h->vt_col, M * 4));
+  DFH_CHECK(dev_alloc(h->cu_rows, (nn + 1) * 4));
+  DFH_CHECK(dev_alloc(h->cu_vt, (nn + 1) * 4));
+  DFH_CHECK(dev_alloc(h->hist_len, nn * 4));
+  DFH_CHECK(dev_alloc(h->counts, 16));
+  DFH_CHECK(dev_alloc(h->err, 16));
+  DFH_CHECK(dev_alloc(h->patch_rows, nn * P * 4));
+  DFH_CHECK(dev_alloc(h->rope_cos, (size_t)TT * 32 * 4));
+  DFH_CHECK(dev_alloc(h->rope_sin, (size_t)TT * 32 * 4));
+  const long RS = (long)SS > nn ? SS : nn;  // timestep rows: per step (solve) or per request (forward)
+  DFH_CHECK(dev_alloc(h->temb_in, RS * c.freq_dim * 2));
+  DFH_CHECK(dev_alloc(h->t_hid, RS * H * 2));
+  DFH_CHECK(dev_alloc(h->t_out, RS * H * 2));
+  DFH_CHECK(dev_alloc(h->d_hid, RS * H * 2));
+  DFH_CHECK(dev_alloc(h->d_out, RS * H * 2));
+  DFH_CHECK(dev_alloc(h->cond, (long)SS * nn * H * 2));
+  DFH_CHECK(dev_alloc(h->cond_act, (long)SS * nn * H * 2));
+  DFH_CHECK(dev_alloc(h->mod, (long)SS * nn * h->ld_mod * 2));
+  DFH_CHECK(dev_alloc(h->z, nn * P * ld * 2));
+  DFH_CHECK(dev_alloc(h->zp, nn * P * H * 2));
+  DFH_CHECK(dev_alloc(h->fin, M * H * 2));
+  DFH_CHECK(dev_alloc(h->vel, M * ld * 2));
+  DFH_CHECK(dev_alloc(h->tvals, (size_t)(2 * RS + 64) * 4));
+  h->cap_n = nn;
+  h->cap_T = TT;
+  h->cap_S = SS;
+  h->cap_M = M;
+  h->ld_vt = ld_vt;
+  return 0;
+}
+
+// c-vector pipeline: timestep rows tv[0..R) (device floats, t then dt), condition
+// and every block's adaLN modulation for rows (s, i) -> mod[(s*N + i)].
+int build_modulation(DfhHandle* h, int S, int N, bool per_request_t, const float* t_dev,
+                     const float* dt_dev, const TimeVals& t_host, const TimeVals& dt_host, bool has_dt,
+                     const uint16_t* g, hipStream_t s) {
+  const DfhConfig& c = h->cfg;
+  const int H = c.hidden, fd = c.freq_dim;
+  const int R = per_request_t ? N : S;  // timestep rows
+  const float* freqs = P<float>(h->consts) + (c.rotary ? c.head_dim / 2 : 0);
+  DFH_CHECK(timestep_embed(t_dev, t_host, R, freqs, fd / 2, fd, P<uint16_t>(h->temb_in), s));
+  // time MLP: Linear(fd->H) -> SiLU -> Linear(H->H)
+  DFH_CHECK(gemm(h, PC_OTHER, linear_args(P<uint16_t>(h->temb_in), fd, h->t_w0, h->t_b0,
+                                          P<uint16_t>(h->t_hid), H, R, nullptr, H, fd), EPI_BIAS, s));
+  DFH_CHECK(silu_bf16(P<uint16_t>(h->t_hid), P<uint16_t>(h->t_hid), (long)R * H, s));
+  DFH_CHECK(gemm(h, PC_OTHER, linear_args(P<uint16_t>(h->t_hid), H, h->t_w2, h->t_b2,
+                                          P<uint16_t>(h->t_out), H, R, nullptr, H, H), EPI_BIAS, s));
+  const uint16_t* demb = nullptr;
+  if (c.meanflow && has_dt) {
+    DFH_CHECK(timestep_embed(dt_dev, dt_host, R, freqs, fd / 2, fd, P<uint16_t>(h->temb_in), s));
+    DFH_CHECK(gemm(h, PC_OTHER, linear_args(P<uint16_t>(h->temb_in), fd, h->d_w0, h->d_b0,
+                                            P<uint16_t>(h->d_hid), H, R, nullptr, H, fd), EPI_BIAS, s));
+    DFH_CHECK(silu_bf16(P<uint16_t>(h->d_hid), P<uint16_t>(h->d_hid), (long)R * H, s));
+    DFH_CHECK(gemm(h, PC_OTHER, linear_args(P<uint16_t>(h->d_hid), H, h->d_w2, h->d_b2,
+                                            P<uint16_t>(h->d_out), H, R, nullptr, H, H), EPI_BIAS, s));
+    demb = P<uint16_t>(h->d_out);
+  }
+  DFH_CHECK(condition(P<uint16_t>(h->t_out), demb, g, per_request_t ? 1 : S, N, H,
+                      P<uint16_t>(h->cond), P<uint16_t>(h->cond_act), s, per_request_t));
+  // every block's adaLN (and the final layer's) in one GEMM: [S*N, H] x [ld_mod, H]^T
+  DFH_CHECK(gemm(h, PC_OTHER, linear_args(P<uint16_t>(h->cond_act), H, h->ada_w, h->ada_b,
+                                          P<uint16_t>(h->mod), h->ld_mod,
+                                          (per_request_t ? 1 : S) * N, nullptr, h->ld_mod, H),
+                 EPI_BIAS, s));
+  return 0;
+}
+
+// One DiT forward over the packed rows held in h->seq (M rows, device count in
+// counts[0]); modulation rows for this pass start at mod_row0 (request i uses
+// row mod_row0 + i). Writes the block output to h->x.
+int dit_blocks(DfhHandle* h, int n, int T, long mod_row0, hipStream_t s) {
+  const DfhConfig& c = h->cfg;
+  const int H = c.hidden, F = c.ffn;
+  const int Mup = n * T;
+  const int* Md = P<int>(h->counts);
+  const uint16_t* mod = P<uint16_t>(h->mod) + mod_row0 * h->ld_mod;
+  const long ldm = h->ld_mod;
+  int* row_req = P<int>(h->row_req);
+
+  // input_layer
+  DFH_CHECK(gemm(h, PC_OTHER, linear_args(P<uint16_t>(h->seq), H, h->in_w, h->in_b,
+                                          P<uint16_t>(h->x), H, Mup, Md, H, H), EPI_BIAS, s));
+  for (int l = 0; l < c.n_blocks; ++l) {
+    const uint16_t* ml = mod + (long)l * 6 * H;  // shift_a, scale_a, gate_a, shift_f, scale_f, gate_f
+    prof_arm(h, PC_LN);
+    DFH_CHECK(ln_modulate(P<uint16_t>(h->x), H, P<uint16_t>(h->hbuf), H, ml + 0 * H, ml + 1 * H, ldm,
+                          row_req, nullptr, Mup, Md, H, c.ln_eps, s));
+    GemmArgs q = linear_args(P<uint16_t>(h->hbuf), H, h->qkv_w[l], h->qkv_b[l], P<uint16_t>(h->qk),
+                             2 * H, Mup, Md, 3 * H, H);
+    q.hidden = H; q.head_dim = c.head_dim;
+    q.rope_cos = c.rotary ? P<float>(h->rope_cos) : nullptr;
+    q.rope_sin = c.rotary ? P<float>(h->rope_sin) : nullptr;
+    q.row_pos = P<int>(h->row_pos);
+    q.qk_norm = c.qk_norm;
+    q.qn_w = h->qn_w[l]; q.qn_b = h->qn_b[l]; q.kn_w = h->kn_w[l]; q.kn_b = h->kn_b[l];
+    q.vt = P<uint16_t>(h->vt); q.ld_vt = h->ld_vt; q.vt_col = P<int>(h->vt_col);
+    DFH_CHECK(gemm(h, PC_QKV, q, EPI_QKV, s, 1));
+    prof_arm(h, PC_ATTN);
+    DFH_CHECK(fm_attention(P<uint16_t>(h->qk), 2 * H, P<uint16_t>(h->vt), h->ld_vt,
+                           P<uint16_t>(h->attn), H, P<int>(h->cu_rows), P<int>(h->cu_vt),
+                           P<int>(h->hist_len), n, c.patch, c.heads, T, s));
+    GemmArgs o = linear_args(P<uint16_t>(h->attn), H, h->o_w[l], h->o_b[l], P<uint16_t>(h->x), H,
+                             Mup, Md, H, H);
+    o.gate = ml + 2 * H; o.ld_gate = ldm; o.row_req = row_req;
+    DFH_CHECK(gemm(h, PC_O, o, EPI_GATE_RES, s));
+    prof_arm(h, PC_LN);
+    DFH_CHECK(ln_modulate(P<uint16_t>(h->x), H, P<uint16_t>(h->hbuf), H, ml + 3 * H, ml + 4 * H, ldm,
+                          row_req, nullptr, Mup, Md, H, c.ln_eps, s));
+    DFH_CHECK(gemm(h, PC_FC1, linear_args(P<uint16_t>(h->hbuf), H, h->fc1_w[l], h->fc1_b[l],
+                                          P<uint16_t>(h->ff), F, Mup, Md, F, H), EPI_GELU, s));
+    GemmArgs f2 = linear_args(P<uint16_t>(h->ff), F, h->fc2_w[l], h->fc2_b[l], P<uint16_t>(h->x), H,
+                              Mup, Md, H, F);
+    f2.gate = ml + 5 * H; f2.ld_gate = ldm; f2.row_req = row_req;
+    DFH_CHECK(gemm(h, PC_FC2, f2, EPI_GATE_RES, s));
+  }
+  return 0;
+}
+
+int layout(DfhHandle* h, int n, int T, const void* pos_ids, const void* inp, hipStream_t s) {
+  const DfhConfig& c = h->cfg;
+  DFH_CHECK(fm_layout(reinterpret_cast<const float*>(pos_ids), n, T, c.patch, P<int>(h->cu_rows),
+                      P<int>(h->cu_vt), P<int>(h->hist_len), P<int>(h->counts), P<int>(h->err), s));
+  DFH_CHECK(fm_gather(reinterpret_cast<const uint16_t*>(inp), n, T, c.patch, c.hidden,
+                      P<int>(h->cu_rows), P<int>(h->cu_vt), P<int>(h->hist_len), P<uint16_t>(h->seq),
+                      P<int>(h->row_req), P<int>(h->row_pos), P<int>(h->vt_col),
+                      P<int>(h->patch_rows), s));
+  if (c.rotary)
+    DFH_CHECK(rope_table(P<float>(h->consts), c.head_dim / 2, T, P<float>(h->rope_cos),
+                         P<float>(h->rope_sin), s));
+  return 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* dfh_last_error(void) { return g_err.c_str(); }
+
+int dfh_create(const DfhConfig* cfg, DfhHandle** out) {
+  if (!cfg || !out) return fail("null argument");
+  if (check_cfg(*cfg)) return 1;
+  DfhHandle* h = new DfhHandle();
+  h->cfg = *cfg;
+  if (cfg->rotary) h->rope_inv_freq.assign(cfg->rope_inv_freq, cfg->rope_inv_freq + cfg->head_dim / 2);
+  h->temb_freqs.assign(cfg->temb_freqs, cfg->temb_freqs + cfg->freq_dim / 2);
+  h->cfg.rope_inv_freq = nullptr;
+  h->cfg.temb_freqs = nullptr;
+  h->ld_mod = cfg->n_blocks * 6 * cfg->hidden + 2 * cfg->hidden;
+  std::vector<float> consts(h->rope_inv_freq);
+  consts.insert(consts.end(), h->temb_freqs.begin(), h->temb_freqs.end());
+  hipError_t e = dev_alloc(h->consts, consts.size() * 4);
+  if (e == hipSuccess) e = hipMemcpy(h->consts.p, consts.data(), consts.size() * 4, hipMemcpyHostToDevice);
+  if (e != hipSuccess) {
+    delete h;
+    return fail("dfh_create: %s", hipGetErrorString(e));
+  }
+  *out = h;
+  return 0;
+}
+
+int dfh_destroy(DfhHandle* h) {
+  if (!h) return 0;
+  (void)hipDeviceSynchronize();
+  DevBuf* bufs[] = {&h->w_arena, &h->consts, &h->seq, &h->x, &h->hbuf, &h->qk, &h->attn, &h->ff,
+                    &h->vt, &h->row_req, &h->row_pos, &h->vt_col, &h->cu_rows, &h->cu_vt,
+                    &h->hist_len, &h->counts, &h->err, &h->patch_rows, &h->rope_cos, &h->rope_sin,
+                    &h->temb_in, &h->t_hid, &h->t_out, &h->d_hid, &h->d_out, &h->cond,
+                    &h->cond_act, &h->mod, &h->z, &h->zp, &h->fin, &h->vel, &h->tvals};
+  for (DevBuf* b : bufs)
+    if (b->p) (void)hipFree(b->p);
+  for (hipEvent_t ev : h->ev_pool) (void)hipEventDestroy(ev);
+  delete h;
+  return 0;
+}
+
+int dfh_set_weights(DfhHandle* h, const DfhWeights* w, void* stream) {
+  if (!h || !w || !w->blocks) return fail("null argument");
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const DfhConfig& c = h->cfg;
+  const long H = c.hidden, F = c.ffn, ld = c.latent_dim, fd = c.freq_dim, hd = c.head_dim;
+  const int nb = c.n_blocks;
+  if (!w->input_w || !w->input_b || !w->t_w0 || !w->t_b0 || !w->t_w2 || !w->t_b2 || !w->final_ada_w ||
+      !w->final_ada_b || !w->final_w || !w->final_b || !w->coord_w || !w->coord_b)
+    return fail("dfh_set_weights: a required tensor is NULL");
+  if (c.meanflow && (!w->d_w0 || !w->d_b0 || !w->d_w2 || !w->d_b2))
+    return fail("dfh_set_weights: meanflow DiT needs the duration embedder");
+  // arena layout (elements); every piece 256-B aligned
+  struct Piece { const void* src; long elems; const uint16_t** dst; };
+  std::vector<Piece> pieces;
+  std::vector<std::pair<long, long>> zero_fill;  // (offset, elems) for absent biases
+  long off = 0;
+  auto take = [&](long elems) { long o = off; off += (elems + 127) / 128 * 128; return o; };
+  std::vector<long> offs;
+  struct Copy { const void* src; long dst_off; long elems; };
+  std::vector<Copy> copies;
+  auto add = [&](const void* src, long elems) -> long {
+    long o = take(elems);
+    if (src) copies.push_back({src, o, elems});
+    else zero_fill.push_back({o, elems});
+    return o;
+  };
+  const long o_in_w = add(w->input_w, H * H), o_in_b = add(w->input_b, H);
+  const long o_t_w0 = add(w->t_w0, H * fd), o_t_b0 = add(w->t_b0, H);
+  const long o_t_w2 = add(w->t_w2, H * H), o_t_b2 = add(w->t_b2, H);
+  long o_d_w0 = 0, o_d_b0 = 0, o_d_w2 = 0, o_d_b2 = 0;
+  if (c.meanflow) {
+    o_d_w0 = add(w->d_w0, H * fd); o_d_b0 = add(w->d_b0, H);
+    o_d_w2 = add(w->d_w2, H * H); o_d_b2 = add(w->d_b2, H);
+  }
+  // all adaLN rows contiguous: blocks 0..nb-1 (6H each) then the final layer (2H)
+  const long o_ada_w = take((long)h->ld_mod * H);
+  const long o_ada_b = take(h->ld_mod);
+  for (int l = 0; l < nb; ++l) {
+    const DfhBlockWeights& b = w->blocks[l];
+    if (!b.ada_w || !b.ada_b) return fail("block %d: adaLN weights missing", l);
+    copies.push_back({b.ada_w, o_ada_w + (long)l * 6 * H * H, 6 * H * H});
+    copies.push_back({b.ada_b, o_ada_b + (long)l * 6 * H, 6 * H});
+  }
+  copies.push_back({w->final_ada_w, o_ada_w + (long)nb * 6 * H * H, 2 * H * H});
+  copies.push_back({w->final_ada_b, o_ada_b + (long)nb * 6 * H, 2 * H});
+  const long o_fin_w = add(w->final_w, ld * H), o_fin_b = add(w->final_b, ld);
+  const long o_co_w = add(w->coord_w, H * ld), o_co_b = add(w->coord_b, H);
+  std::vector<long> o_qkv_w(nb), o_qkv_b(nb), o_o_w(nb), o_o_b(nb), o_f1w(nb), o_f1b(nb), o_f2w(nb),
+      o_f2b(nb), o_qn_w(nb), o_qn_b(nb), o_kn_w(nb), o_kn_b(nb);
+  for (int l = 0; l < nb; ++l) {
+    const DfhBlockWeights& b = w->blocks[l];
+    if (!b.q_w || !b.k_w || !b.v_w || !b.o_w || !b.o_b || !b.fc1_w || !b.fc1_b || !b.fc2_w || !b.fc2_b)
+      return fail("block %d: a required tensor is NULL", l);
+    o_qkv_w[l] = take(3 * H * H);
+    copies.push_back({b.q_w, o_qkv_w[l], H * H});
+    copies.push_back({b.k_w, o_qkv_w[l] + H * H, H * H});
+    copies.push_back({b.v_w, o_qkv_w[l] + 2 * H * H, H * H});
+    o_qkv_b[l] = -1;
+    if (c.qkv_bias) {
+      if (!b.q_b || !b.k_b || !b.v_b) return fail("block %d: qkv_bias set but a bias is NULL", l);
+      o_qkv_b[l] = take(3 * H);
+      copies.push_back({b.q_b, o_qkv_b[l], H});
+      copies.push_back({b.k_b, o_qkv_b[l] + H, H});
+      copies.push_back({b.v_b, o_qkv_b[l] + 2 * H, H});
+    }
+    o_o_w[l] = add(b.o_w, H * H); o_o_b[l] = add(b.o_b, H);
+    o_f1w[l] = add(b.fc1_w, F * H); o_f1b[l] = add(b.fc1_b, F);
+    o_f2w[l] = add(b.fc2_w, H * F); o_f2b[l] = add(b.fc2_b, H);
+    o_qn_w[l] = o_qn_b[l] = o_kn_w[l] = o_kn_b[l] = -1;
+    if (c.qk_norm) {
+      if (!b.q_norm_w || !b.k_norm_w) return fail("block %d: qk_norm weights missing", l);
+      o_qn_w[l] = add(b.q_norm_w, hd); o_kn_w[l] = add(b.k_norm_w, hd);
+      if (c.qk_norm == 1) {
+        if (!b.q_norm_b || !b.k_norm_b) return fail("block %d: qk LayerNorm biases missing", l);
+        o_qn_b[l] = add(b.q_norm_b, hd); o_kn_b[l] = add(b.k_norm_b, hd);
+      }
+    }
+  }
+  DFH_CHECK(hipStreamSynchronize(s));
+  DFH_CHECK(dev_alloc(h->w_arena, (size_t)off * 2));
+  uint16_t* base = P<uint16_t>(h->w_arena);
+  for (const Copy& cp : copies)
+    DFH_CHECK(hipMemcpyAsync(base + cp.dst_off, cp.src, cp.elems * 2, hipMemcpyDeviceToDevice, s));
+  for (auto& z : zero_fill) DFH_CHECK(hipMemsetAsync(base + z.first, 0, z.second * 2, s));
+  DFH_CHECK(hipStreamSynchronize(s));
+  auto at = [&](long o) -> const uint16_t* { return o < 0 ? nullptr : base + o; };
+  h->in_w = at(o_in_w); h->in_b = at(o_in_b);
+  h->t_w0 = at(o_t_w0); h->t_b0 = at(o_t_b0); h->t_w2 = at(o_t_w2); h->t_b2 = at(o_t_b2);
+  if (c.meanflow) {
+    h->d_w0 = at(o_d_w0); h->d_b0 = at(o_d_b0); h->d_w2 = at(o_d_w2); h->d_b2 = at(o_d_b2);
+  } else {
+    h->d_w0 = h->d_b0 = h->d_w2 = h->d_b2 = nullptr;
+  }
+  h->ada_w = at(o_ada_w); h->ada_b = at(o_ada_b);
+  h->fin_w = at(o_fin_w); h->fin_b = at(o_fin_b);
+  h->coord_w = at(o_co_w); h->coord_b = at(o_co_b);
+  h->qkv_w.resize(nb); h->qkv_b.resize(nb); h->o_w.resize(nb); h->o_b.resize(nb);
+  h->fc1_w.resize(nb); h->fc1_b.resize(nb); h->fc2_w.resize(nb); h->fc2_b.resize(nb);
+  h->qn_w.resize(nb); h->qn_b.resize(nb); h->kn_w.resize(nb); h->kn_b.resize(nb);
+  for (int l = 0; l < nb; ++l) {
+    h->qkv_w[l] = at(o_qkv_w[l]); h->qkv_b[l] = at(o_qkv_b[l]);
+    h->o_w[l] = at(o_o_w[l]); h->o_b[l] = at(o_o_b[l]);
+    h->fc1_w[l] = at(o_f1w[l]); h->fc1_b[l] = at(o_f1b[l]);
+    h->fc2_w[l] = at(o_f2w[l]); h->fc2_b[l] = at(o_f2b[l]);
+    h->qn_w[l] = at(o_qn_w[l]); h->qn_b[l] = at(o_qn_b[l]);
+    h->kn_w[l] = at(o_kn_w[l]); h->kn_b[l] = at(o_kn_b[l]);
+  }
+  h->weights_set = true;
+  return 0;
+}
+
+int dfh_reserve(DfhHandle* h, int n, int T, int S, void* stream) {
+  if (!h) return fail("null handle");
+  if (n <= 0 || n > 1024 || T <= h->cfg.patch || S <= 0 || S > 16)
+    return fail("dfh_reserve: bad shape n=%d T=%d steps=%d", n, T, S);
+  return reserve(h, n, T, S, reinterpret_cast<hipStream_t>(stream));
+}
+
+int dfh_meanflow_solve(DfhHandle* h, const DfhSolveArgs* a, void* stream) {
+  if (!h || !a) return fail("null argument");
+  if (!h->weights_set) return fail("dfh_meanflow_solve: weights not set");
+  const DfhConfig& c = h->cfg;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const int n = a->n, T = a->total_len, S = a->num_steps;
+  if (n <= 0 || n > 1024 || T <= c.patch || S <= 0 || S > 16)
+    return fail("dfh_meanflow_solve: bad shape n=%d T=%d steps=%d", n, T, S);
+  if (!a->input_sequence || !a->pos_ids || !a->noise || !a->out || !a->t_grid || !a->dt_grid)
+    return fail("dfh_meanflow_solve: a required pointer is NULL");
+  if (!c.meanflow) return fail("dfh_meanflow_solve: DiT has no duration embedder (not MeanFlow)");
+  if ((long)n * T * 4 * c.ffn >= (1L << 31))
+    return fail("dfh_meanflow_solve: n*T too large for 32-bit offsets");
+  if (reserve(h, n, T, S, s)) return 1;
+  const int H = c.hidden, Pp = c.patch, ld = c.latent_dim;
+
+  if (layout(h, n, T, a->pos_ids, a->input_sequence, s)) return 1;
+  // timestep rows t_0..t_{S-1} and dt_0..dt_{S-1} travel as kernel arguments
+  TimeVals tv{}, dtv{};
+  for (int k = 0; k < S; ++k) { tv.v[k] = a->t_grid[k]; dtv.v[k] = a->dt_grid[k]; }
+  if (build_modulation(h, S, n, false, nullptr, nullptr, tv, dtv, true,
+                       reinterpret_cast<const uint16_t*>(a->g_cond), s))
+    return 1;
+  DFH_CHECK(hipMemcpyAsync(h->z.p, a->noise, (size_t)n * Pp * ld * 2, hipMemcpyDeviceToDevice, s));
+  const int NP = n * Pp;
+  for (int st = 0; st < S; ++st) {
+    // zp = coordinate_proj(z) -> latent rows of the packed sequence
+    DFH_CHECK(gemm(h, PC_OTHER, linear_args(P<uint16_t>(h->z), ld, h->coord_w, h->coord_b,
+                                            P<uint16_t>(h->zp), H, NP, nullptr, H, ld), EPI_BIAS, s));
+    DFH_CHECK(scatter_rows(P<uint16_t>(h->zp), P<int>(h->patch_rows), NP, H, P<uint16_t>(h->seq), s));
+    if (dit_blocks(h, n, T, (long)st * n, s)) return 1;
+    // FinalLayer on the latent rows only
+    const uint16_t* mf = P<uint16_t>(h->mod) + (long)st * n * h->ld_mod + (long)c.n_blocks * 6 * H;
+    prof_arm(h, PC_LN);
+    DFH_CHECK(ln_modulate(P<uint16_t>(h->x), H, P<uint16_t>(h->fin), H, mf, mf + H, h->ld_mod,
+                          P<int>(h->row_req), P<int>(h->patch_rows), NP, nullptr, H, c.ln_eps, s));
+    DFH_CHECK(gemm(h, PC_OTHER, linear_args(P<uint16_t>(h->fin), H, h->fin_w, h->fin_b,
+                                            P<uint16_t>(h->vel), ld, NP, nullptr, ld, H), EPI_BIAS, s));
+    DFH_CHECK(z_update(P<uint16_t>(h->z), P<uint16_t>(h->vel), a->dt_grid[st], (long)NP * ld, s));
+  }
+  DFH_CHECK(hipMemcpyAsync(a->out, h->z.p, (size_t)NP * ld * 2, hipMemcpyDeviceToDevice, s));
+  return 0;
+}
+
+int dfh_dit_forward(DfhHandle* h, const DfhForwardArgs* a, void* stream) {
+  if (!h || !a) return fail("null argument");
+  if (!h->weights_set) return fail("dfh_dit_forward: weights not set");
+  const DfhConfig& c = h->cfg;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const int n = a->n, T = a->total_len;
+  if (n <= 0 || n > 1024 || T <= c.patch) return fail("dfh_dit_forward: bad shape n=%d T=%d", n, T);
+  if (!a->x || !a->timesteps || !a->pos_ids || !a->out) return fail("dfh_dit_forward: NULL pointer");
+  if ((long)n * T * 4 * c.ffn >= (1L << 31)) return fail("dfh_dit_forward: n*T too large");
+  if (reserve(h, n, T, 1, s)) return 1;
+  const int H = c.hidden, Pp = c.patch, ld = c.latent_dim;
+  if (layout(h, n, T, a->pos_ids, a->x, s)) return 1;
+  TimeVals none{};
+  const bool has_dt = c.meanflow && a->duration != nullptr;
+  if (build_modulation(h, 1, n, true, reinterpret_cast<const float*>(a->timesteps),
+                       reinterpret_cast<const float*>(a->duration), none, none, has_dt,
+                       reinterpret_cast<const uint16_t*>(a->g_cond), s))
+    return 1;
+  if (dit_blocks(h, n, T, 0, s)) return 1;
+  // FinalLayer on every packed row, then scatter back to the padded layout
+  const int Mup = n * T;
+  const uint16_t* mf = P<uint16_t>(h->mod) + (long)c.n_blocks * 6 * H;
+  DFH_CHECK(ln_modulate(P<uint16_t>(h->x), H, P<uint16_t>(h->fin), H, mf, mf + H, h->ld_mod,
+                        P<int>(h->row_req), nullptr, Mup, P<int>(h->counts), H, c.ln_eps, s));
+  DFH_CHECK(gemm(h, PC_OTHER, linear_args(P<uint16_t>(h->fin), H, h->fin_w, h->fin_b,
+                                          P<uint16_t>(h->vel), ld, Mup, P<int>(h->counts), ld, H),
+                 EPI_BIAS, s));
+  DFH_CHECK(dfh::unpack_rows(P<uint16_t>(h->vel), n, T, Pp, ld, P<int>(h->cu_rows), P<int>(h->hist_len),
+                             reinterpret_cast<uint16_t*>(a->out), s));
+  return 0;
+}
+
+int dfh_input_status(DfhHandle* h, int* flags, void* stream) {
+  if (!h || !flags) return fail("null argument");
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  *flags = 0;
+  if (!h->err.p) return 0;
+  DFH_CHECK(hipMemcpyAsync(flags, h->err.p, 4, hipMemcpyDeviceToHost, s));
+  DFH_CHECK(hipStreamSynchronize(s));
+  DFH_CHECK(hipMemsetAsync(h->err.p, 0, 4, s));
+  DFH_CHECK(hipStreamSynchronize(s));
+  return 0;
+}
+
+int dfh_profile_enable(DfhHandle* h, int enable) {
+  if (!h) return fail("null handle");
+  if (enable && h->ev_pool.empty()) {
+    h->ev_pool.resize(1 << 14);
+    for (auto& ev : h->ev_pool) DFH_CHECK(hipEventCreate(&ev));
+  }
+  h->prof = enable != 0;
+  return 0;
+}
+
+int dfh_profile_read(DfhHandle* h, double* ms, long* cnt, int n_classes) {
+  if (!h) return fail("null handle");
+  for (auto& u : h->ev_used) {
+    DFH_CHECK(hipEventSynchronize(h->ev_pool[u.second + 1]));
+    float t = 0.f;
+    DFH_CHECK(hipEventElapsedTime(&t, h->ev_pool[u.second], h->ev_pool[u.second + 1]));
+    h->prof_ms[u.first] += t;
+    h->prof_n[u.first] += 1;
+  }
+  h->ev_used.clear();
+  h->ev_next = 0;
+  for (int i = 0; i < n_classes && i < PC_N; ++i) {
+    if (ms) ms[i] = h->prof_ms[i];
+    if (cnt) cnt[i] = h->prof_n[i];
+    h->prof_ms[i] = 0;
+    h->prof_n[i] = 0;
+  }
+  return 0;
+}
+
+int dfh_gemm_bf16(const void* A, long lda, const void* B, long ldb, void* C, long ldc, const void* bias,
+                  int M, int N, int K, int epilogue, int tile, void* stream) {
+  if (!A || !B || !C) return fail("dfh_gemm_bf16: NULL pointer");
+  if (epilogue != EPI_BIAS && epilogue != EPI_GELU && epilogue != EPI_F32)
+    return fail("dfh_gemm_bf16: epilogue %d not exposed", epilogue);
+  if (lda % 8 || ldb % 8 || ldc % 8 || lda < K || ldb < K || ldc < N)
+    return fail("dfh_gemm_bf16: leading dimensions must be >= the row length and multiples of 8");
+  GemmArgs a;
+  memset(&a, 0, sizeof(a));
+  a.A = reinterpret_cast<const uint16_t*>(A); a.lda = lda;
+  a.B = reinterpret_cast<const uint16_t*>(B); a.ldb = ldb;
+  a.C = reinterpret_cast<uint16_t*>(C); a.Cf = reinterpret_cast<float*>(C); a.ldc = ldc;
+  a.bias = reinterpret_cast<const uint16_t*>(bias);
+  a.M = M; a.N = N; a.K = K;
+  hipError_t e = gemm_bf16(a, epilogue, reinterpret_cast<hipStream_t>(stream), tile);
+  if (e != hipSuccess) return fail("dfh_gemm_bf16(M=%d N=%d K=%d tile=%d): %s", M, N, K, tile,
+                                   hipGetErrorString(e));
+  return 0;
+}
+
+}  // extern "C"

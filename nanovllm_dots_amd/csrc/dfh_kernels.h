@@ -1,0 +1,79 @@
+// Host-side launch interface of the FM/DiT head kernels (internal to the library).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace dfh {
+
+// Dispatch-packet timing: when both events are set, the next kernel launched by a
+// dfh launcher records them (hipExtLaunchKernelGGL) and the slot is cleared.
+struct LaunchEvents {
+  hipEvent_t start = nullptr, stop = nullptr;
+};
+extern thread_local LaunchEvents g_launch_events;
+
+// launch helper honouring g_launch_events
+template <typename K, typename... Args>
+inline void dfh_launch(K kernel, dim3 grid, dim3 block, unsigned shmem, hipStream_t s, Args... args);
+
+enum Epilogue : int {
+  EPI_BIAS = 0,      // C = bf16(acc + bias)
+  EPI_GELU = 1,      // C = bf16(gelu_tanh(bf16(acc + bias)))
+  EPI_GATE_RES = 2,  // C = bf16(C + bf16(gate[req(m)] * bf16(acc + bias)))   (in place)
+  EPI_QKV = 3,       // q|k -> C (optional qk-norm, RoPE), v -> V^T (transposed)
+  EPI_F32 = 4,       // Cf = acc + bias (float32 out; tests)
+};
+
+struct GemmArgs {
+  const uint16_t* A; long lda;       // [M, K] bf16 activations, K contiguous
+  const uint16_t* B; long ldb;       // [N, K] bf16 weights (nn.Linear layout)
+  uint16_t* C; long ldc;             // [M, N] bf16 output
+  float* Cf;                         // float32 output (EPI_F32)
+  const uint16_t* bias;              // [N] or null
+  int M; const int* M_dev;           // rows; M_dev (device int) overrides M when non-null
+  int N, K;
+  // EPI_GATE_RES
+  const uint16_t* gate; long ld_gate; const int* row_req;
+  // EPI_QKV
+  int hidden, head_dim;
+  const float* rope_cos; const float* rope_sin;  // [max_pos, head_dim/2] or null (no rotary)
+  const int* row_pos;                            // [M] position of each row within its request
+  int qk_norm;                                   // 0 none, 1 LayerNorm(affine), 2 RMSNorm
+  const uint16_t* qn_w; const uint16_t* qn_b;    // [head_dim]
+  const uint16_t* kn_w; const uint16_t* kn_b;
+  uint16_t* vt; long ld_vt; const int* vt_col;   // V^T [hidden, ld_vt]; column of row m = vt_col[m]
+};
+
+// Picks a tile shape for (M, N, K) and launches the persistent MFMA kernel.
+// Returns hipSuccess or an error (shape not supported / launch failure).
+hipError_t gemm_bf16(const GemmArgs& a, int epi, hipStream_t s, int tile_hint = -1);
+
+// Row kernels -------------------------------------------------------------------
+// LayerNorm (no affine, fp32 stats) + adaLN modulate:
+//   out[m] = bf16( LN(x[m]) * bf16(1 + scale[req]) + shift[req] )
+hipError_t ln_modulate(const uint16_t* x, long ldx, uint16_t* out, long ldo,
+                       const uint16_t* shift, const uint16_t* scale, long ld_mod,
+                       const int* row_req, const int* row_map, int rows_upper, const int* M_dev,
+                       int H, float eps, hipStream_t s);
+
+// Varlen FM-mask attention (head_dim 64). qk: [M, 2H] (q | k), vt: [H, ld_vt].
+hipError_t fm_attention(const uint16_t* qk, long ldqk, const uint16_t* vt, long ld_vt,
+                        uint16_t* out, long ldo, const int* cu_rows, const int* cu_vt,
+                        const int* hist_len, int n_req, int patch, int heads, int max_T,
+                        hipStream_t s);
+
+}  // namespace dfh
+
+#include <hip/hip_ext.h>
+namespace dfh {
+template <typename K, typename... Args>
+inline void dfh_launch(K kernel, dim3 grid, dim3 block, unsigned shmem, hipStream_t s, Args... args) {
+  if (g_launch_events.start) {
+    hipEvent_t a = g_launch_events.start, b = g_launch_events.stop;
+    g_launch_events.start = g_launch_events.stop = nullptr;
+    hipExtLaunchKernelGGL(kernel, grid, block, shmem, s, a, b, 0, args...);
+  } else {
+    hipLaunchKernelGGL(kernel, grid, block, shmem, s, args...);
+  }
+}
+}  // namespace dfh

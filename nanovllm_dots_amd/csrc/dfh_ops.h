@@ -1,0 +1,31 @@
+// Host launchers of the row / elementwise kernels (internal to the library).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace dfh {
+
+constexpr int kMaxTimeVals = 16;
+struct TimeVals {
+  float v[kMaxTimeVals];
+};
+
+hipError_t fm_layout(const float* pos_ids, int n, int T, int P, int* cu_rows, int* cu_vt,
+                     int* hist_len, int* counts, int* err, hipStream_t s);
+hipError_t fm_gather(const uint16_t* inp, int n, int T, int P, int H, const int* cu_rows,
+                     const int* cu_vt, const int* hist_len, uint16_t* seq, int* row_req,
+                     int* row_pos, int* vt_col, int* patch_rows, hipStream_t s);
+hipError_t rope_table(const float* inv_freq, int half, int max_pos, float* cosv, float* sinv,
+                      hipStream_t s);
+hipError_t timestep_embed(const float* tv, const TimeVals& tvh, int rows, const float* freqs, int half,
+                          int dim, uint16_t* out, hipStream_t s);
+hipError_t silu_bf16(const uint16_t* x, uint16_t* y, long n, hipStream_t s);
+hipError_t condition(const uint16_t* temb, const uint16_t* demb, const uint16_t* g, int S, int N,
+                     int H, uint16_t* c_out, uint16_t* a_out, hipStream_t s, bool per_request_t);
+hipError_t unpack_rows(const uint16_t* src, int n, int T, int P, int D, const int* cu_rows,
+                       const int* hist_len, uint16_t* dst, hipStream_t s);
+hipError_t scatter_rows(const uint16_t* src, const int* rows_idx, int rows, int H, uint16_t* dst,
+                        hipStream_t s);
+hipError_t z_update(uint16_t* z, const uint16_t* v, float dt, long n, hipStream_t s);
+
+}  // namespace dfh

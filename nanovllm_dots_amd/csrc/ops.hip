@@ -1,0 +1,322 @@
+// Row and elementwise kernels of the FM/DiT head (HBM-bound; one wave per row).
+#include "dfh_device.h"
+#include "dfh_kernels.h"
+#include "dfh_ops.h"
+
+namespace dfh {
+
+namespace {
+
+// ---------------------------------------------------------------------------
+// LayerNorm (no affine, eps) + adaLN modulate, one wave per row.
+// DiTBlock.forward / FinalLayer.forward (nanovllm_dots/models/dots/native/dit.py:
+// 99-105, 60-63) under bf16 autocast: LN in fp32, (1 + scale) rounded to bf16,
+// fp32 product and sum, one rounding to bf16 at the consumer's input.
+template <int VPT>  // values per lane = H / 64, multiple of 4
+__global__ void __launch_bounds__(256)
+ln_modulate_kernel(const uint16_t* __restrict__ x, long ldx, uint16_t* __restrict__ out, long ldo,
+                   const uint16_t* __restrict__ shift, const uint16_t* __restrict__ scale,
+                   long ld_mod, const int* __restrict__ row_req, const int* __restrict__ row_map,
+                   int rows, const int* __restrict__ M_dev, int H, float eps) {
+  const int lane = threadIdx.x & 63;
+  const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int nrows = M_dev ? *M_dev : rows;
+  if (r >= nrows) return;
+  const int src = row_map ? row_map[r] : r;
+  const int req = row_req[src];
+  const uint16_t* xp = x + (long)src * ldx;
+  float v[VPT];
+#pragma unroll
+  for (int j = 0; j < VPT / 4; ++j) {
+    const int col = (j * 64 + lane) * 4;
+    unpack4(*reinterpret_cast<const uint2*>(xp + col), v + 4 * j);
+  }
+  float s = 0.f;
+#pragma unroll
+  for (int j = 0; j < VPT; ++j) s += v[j];
+  const float mean = wave_sum(s) / (float)H;
+  float s2 = 0.f;
+#pragma unroll
+  for (int j = 0; j < VPT; ++j) {
+    const float d = v[j] - mean;
+    s2 += d * d;
+  }
+  const float var = wave_sum(s2) / (float)H;
+  const float rstd = rsqrtf(var + eps);
+  const uint16_t* shp = shift + (long)req * ld_mod;
+  const uint16_t* scp = scale + (long)req * ld_mod;
+  uint16_t* op = out + (long)r * ldo;
+#pragma unroll
+  for (int j = 0; j < VPT / 4; ++j) {
+    const int col = (j * 64 + lane) * 4;
+    float sh[4], sc[4], y[4];
+    unpack4(*reinterpret_cast<const uint2*>(shp + col), sh);
+    unpack4(*reinterpret_cast<const uint2*>(scp + col), sc);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const float ln = __fmul_rn(v[4 * j + t] - mean, rstd);
+      const float onep = rbf(1.0f + sc[t]);
+      y[t] = __fadd_rn(__fmul_rn(ln, onep), sh[t]);
+    }
+    *reinterpret_cast<uint2*>(op + col) = pack4(y[0], y[1], y[2], y[3]);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Request layout from the padded inputs: c_i = pos_ids[i, T-P] (the first latent
+// row's position equals the history length, native/model.py:77-87).
+// One workgroup of up to 1024 threads, one thread per request.
+__global__ void __launch_bounds__(1024)
+fm_layout_kernel(const float* __restrict__ pos_ids, int n, int T, int P, int* __restrict__ cu_rows,
+                 int* __restrict__ cu_vt, int* __restrict__ hist_len, int* __restrict__ counts,
+                 int* __restrict__ err) {
+  __shared__ int s_rows[1024], s_vt[1024];
+  const int i = threadIdx.x;
+  int c = 0;
+  if (i < n) {
+    const float pv = pos_ids[(long)i * T + (T - P)];
+    c = (int)pv;
+    if (!(pv >= 1.0f) || c > T - P || (float)c != pv) {
+      atomicOr(err, 1);
+      c = c < 1 ? 1 : (c > T - P ? T - P : c);
+    }
+    hist_len[i] = c;
+  }
+  const int Ti = i < n ? c + P : 0;
+  s_rows[i] = Ti;
+  s_vt[i] = (Ti + 7) & ~7;
+  __syncthreads();
+  // inclusive Hillis-Steele scan
+  for (int o = 1; o < 1024; o <<= 1) {
+    int a = i >= o ? s_rows[i - o] : 0;
+    int b = i >= o ? s_vt[i - o] : 0;
+    __syncthreads();
+    s_rows[i] += a;
+    s_vt[i] += b;
+    __syncthreads();
+  }
+  if (i < n) {
+    cu_rows[i + 1] = s_rows[i];
+    cu_vt[i + 1] = s_vt[i];
+  }
+  if (i == 0) {
+    cu_rows[0] = 0;
+    cu_vt[0] = 0;
+    counts[0] = s_rows[n - 1];           // M: packed rows
+    counts[1] = s_vt[n - 1];             // V^T columns used
+  }
+}
+
+// Padded [N, T, H] -> packed rows; builds row tables. One wave per padded row.
+__global__ void __launch_bounds__(256)
+fm_gather_kernel(const uint16_t* __restrict__ inp, int n, int T, int P, int H,
+                 const int* __restrict__ cu_rows, const int* __restrict__ cu_vt,
+                 const int* __restrict__ hist_len, uint16_t* __restrict__ seq, int* __restrict__ row_req,
+                 int* __restrict__ row_pos, int* __restrict__ vt_col, int* __restrict__ patch_rows) {
+  const int lane = threadIdx.x & 63;
+  const long pr = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (pr >= (long)n * T) return;
+  const int i = (int)(pr / T), r = (int)(pr % T);
+  const int c = hist_len[i];
+  int local;
+  if (r < c) local = r;
+  else if (r >= T - P) local = c + (r - (T - P));
+  else return;  // padding gap
+  const int dst = cu_rows[i] + local;
+  if (lane == 0) {
+    row_req[dst] = i;
+    row_pos[dst] = local;
+    vt_col[dst] = cu_vt[i] + local;
+    if (local >= c) patch_rows[i * P + (local - c)] = dst;
+  }
+  const uint16_t* sp = inp + pr * H;
+  uint16_t* dp = seq + (long)dst * H;
+  for (int col = lane * 8; col < H; col += 64 * 8)
+    *reinterpret_cast<uint4*>(dp + col) = *reinterpret_cast<const uint4*>(sp + col);
+}
+
+// packed [M, D] rows -> padded [n, T, D]; rows of the padding gap are zero-filled.
+__global__ void unpack_rows_kernel(const uint16_t* __restrict__ src, int n, int T, int P, int D,
+                                   const int* __restrict__ cu_rows, const int* __restrict__ hist_len,
+                                   uint16_t* __restrict__ dst) {
+  const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;  // over n*T*D/4
+  const long total = (long)n * T * (D / 4);
+  if (idx >= total) return;
+  const long pr = idx / (D / 4);
+  const int col = (int)(idx % (D / 4)) * 4;
+  const int i = (int)(pr / T), r = (int)(pr % T);
+  const int c = hist_len[i];
+  int local = -1;
+  if (r < c) local = r;
+  else if (r >= T - P) local = c + (r - (T - P));
+  uint2 v = make_uint2(0u, 0u);
+  if (local >= 0) v = *reinterpret_cast<const uint2*>(src + (long)(cu_rows[i] + local) * D + col);
+  *reinterpret_cast<uint2*>(dst + pr * D + col) = v;
+}
+
+// RoPE tables: cos/sin of pos * inv_freq[d] in fp32 (native/layers.py:124-134), [max_pos, hd/2]
+__global__ void rope_table_kernel(const float* __restrict__ inv_freq, int half, int max_pos,
+                                  float* __restrict__ cosv, float* __restrict__ sinv) {
+  const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= max_pos * half) return;
+  const int p = idx / half, d = idx % half;
+  const float f = __fmul_rn((float)p, inv_freq[d]);
+  cosv[idx] = cosf(f);
+  sinv[idx] = sinf(f);
+}
+
+// Sinusoidal timestep embedding (native/dit.py:34-43): row r has value tv[r];
+// [cos(t*f_k) | sin(t*f_k)] rounded to bf16 (the next Linear's input).
+// Timestep values come from device memory (tv non-null) or by value (tvh).
+__global__ void temb_kernel(const float* __restrict__ tv, TimeVals tvh, int rows,
+                            const float* __restrict__ freqs, int half, int dim,
+                            uint16_t* __restrict__ out) {
+  const int r = blockIdx.x;
+  if (r >= rows) return;
+  const float t = tv ? tv[r] : tvh.v[r];
+  for (int k = threadIdx.x; k < dim; k += blockDim.x) {
+    float e = 0.f;
+    if (k < half) e = cosf(__fmul_rn(t, freqs[k]));
+    else if (k < 2 * half) e = sinf(__fmul_rn(t, freqs[k - half]));
+    out[(long)r * dim + k] = f2bf(e);
+  }
+}
+
+// y = bf16(silu(x)) elementwise over n values
+__global__ void silu_kernel(const uint16_t* __restrict__ x, uint16_t* __restrict__ y, long n) {
+  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) y[i] = f2bf(silu_f(bf2f(x[i])));
+}
+
+// c[s, i] = bf16(bf16(T[s] + D[s]) + g[i]);  a[s*N + i] = bf16(silu(c))
+// (per_req: timestep row i instead of s, i.e. one timestep per request)
+__global__ void condition_kernel(const uint16_t* __restrict__ temb, const uint16_t* __restrict__ demb,
+                                 const uint16_t* __restrict__ g, int S, int N, int H, int per_req,
+                                 uint16_t* __restrict__ c_out, uint16_t* __restrict__ a_out) {
+  const int row = blockIdx.x;  // s*N + i
+  if (row >= S * N) return;
+  const int s = row / N, i = row % N;
+  const int tr = per_req ? i : s;
+  for (int k = threadIdx.x; k < H; k += blockDim.x) {
+    float c = bf2f(temb[(long)tr * H + k]);
+    if (demb) c = rbf(c + bf2f(demb[(long)tr * H + k]));
+    if (g) c = rbf(c + bf2f(g[(long)i * H + k]));
+    c_out[(long)row * H + k] = f2bf(c);
+    a_out[(long)row * H + k] = f2bf(silu_f(c));
+  }
+}
+
+// seq[patch_rows[r]] = src[r]   (rows of H bf16)
+__global__ void scatter_rows_kernel(const uint16_t* __restrict__ src, const int* __restrict__ rows_idx,
+                                    int rows, int H, uint16_t* __restrict__ dst) {
+  const int lane = threadIdx.x & 63;
+  const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (r >= rows) return;
+  const uint16_t* sp = src + (long)r * H;
+  uint16_t* dp = dst + (long)rows_idx[r] * H;
+  for (int col = lane * 8; col < H; col += 64 * 8)
+    *reinterpret_cast<uint4*>(dp + col) = *reinterpret_cast<const uint4*>(sp + col);
+}
+
+// z = bf16(z + bf16(v * dt))  (batched_fm.py:125 in bf16)
+__global__ void z_update_kernel(uint16_t* __restrict__ z, const uint16_t* __restrict__ v, float dt,
+                                long n) {
+  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) z[i] = f2bf(bf2f(z[i]) + rbf(bf2f(v[i]) * dt));
+}
+
+}  // namespace
+
+hipError_t ln_modulate(const uint16_t* x, long ldx, uint16_t* out, long ldo, const uint16_t* shift,
+                       const uint16_t* scale, long ld_mod, const int* row_req, const int* row_map,
+                       int rows_upper, const int* M_dev, int H, float eps, hipStream_t s) {
+  if (rows_upper <= 0) return hipSuccess;
+  if (H % 256 != 0) return hipErrorInvalidValue;
+  dim3 grid((rows_upper + 3) / 4), block(256);
+  switch (H / 64) {
+#define DFH_LN(V)                                                                           \
+  case V:                                                                                  \
+    dfh_launch(ln_modulate_kernel<V>, grid, block, 0, s, x, ldx, out, ldo, shift, \
+                       scale, ld_mod, row_req, row_map, rows_upper, M_dev, H, eps);        \
+    break;
+    DFH_LN(4)
+    DFH_LN(8)
+    DFH_LN(16)
+    DFH_LN(24)
+    DFH_LN(32)
+#undef DFH_LN
+    default:
+      return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+hipError_t fm_layout(const float* pos_ids, int n, int T, int P, int* cu_rows, int* cu_vt,
+                     int* hist_len, int* counts, int* err, hipStream_t s) {
+  if (n <= 0 || n > 1024) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(fm_layout_kernel, dim3(1), dim3(1024), 0, s, pos_ids, n, T, P, cu_rows, cu_vt,
+                     hist_len, counts, err);
+  return hipGetLastError();
+}
+
+hipError_t fm_gather(const uint16_t* inp, int n, int T, int P, int H, const int* cu_rows,
+                     const int* cu_vt, const int* hist_len, uint16_t* seq, int* row_req,
+                     int* row_pos, int* vt_col, int* patch_rows, hipStream_t s) {
+  const long rows = (long)n * T;
+  if (H % 8 != 0) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(fm_gather_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, s, inp, n, T,
+                     P, H, cu_rows, cu_vt, hist_len, seq, row_req, row_pos, vt_col, patch_rows);
+  return hipGetLastError();
+}
+
+hipError_t rope_table(const float* inv_freq, int half, int max_pos, float* cosv, float* sinv,
+                      hipStream_t s) {
+  const int n = half * max_pos;
+  hipLaunchKernelGGL(rope_table_kernel, dim3((n + 255) / 256), dim3(256), 0, s, inv_freq, half,
+                     max_pos, cosv, sinv);
+  return hipGetLastError();
+}
+
+hipError_t timestep_embed(const float* tv, const TimeVals& tvh, int rows, const float* freqs, int half,
+                          int dim, uint16_t* out, hipStream_t s) {
+  if (!tv && rows > kMaxTimeVals) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(temb_kernel, dim3(rows), dim3(256), 0, s, tv, tvh, rows, freqs, half, dim, out);
+  return hipGetLastError();
+}
+
+hipError_t silu_bf16(const uint16_t* x, uint16_t* y, long n, hipStream_t s) {
+  hipLaunchKernelGGL(silu_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, x, y, n);
+  return hipGetLastError();
+}
+
+hipError_t condition(const uint16_t* temb, const uint16_t* demb, const uint16_t* g, int S, int N,
+                     int H, uint16_t* c_out, uint16_t* a_out, hipStream_t s, bool per_request_t) {
+  hipLaunchKernelGGL(condition_kernel, dim3(S * N), dim3(256), 0, s, temb, demb, g, S, N, H,
+                     per_request_t ? 1 : 0, c_out, a_out);
+  return hipGetLastError();
+}
+
+hipError_t scatter_rows(const uint16_t* src, const int* rows_idx, int rows, int H, uint16_t* dst,
+                        hipStream_t s) {
+  if (rows <= 0) return hipSuccess;
+  if (H % 8 != 0) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(scatter_rows_kernel, dim3((rows + 3) / 4), dim3(256), 0, s, src, rows_idx, rows,
+                     H, dst);
+  return hipGetLastError();
+}
+
+hipError_t z_update(uint16_t* z, const uint16_t* v, float dt, long n, hipStream_t s) {
+  hipLaunchKernelGGL(z_update_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, z, v, dt, n);
+  return hipGetLastError();
+}
+
+hipError_t unpack_rows(const uint16_t* src, int n, int T, int P, int D, const int* cu_rows,
+                       const int* hist_len, uint16_t* dst, hipStream_t s) {
+  if (D % 4 != 0) return hipErrorInvalidValue;
+  const long total = (long)n * T * (D / 4);
+  hipLaunchKernelGGL(unpack_rows_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, src, n,
+                     T, P, D, cu_rows, hist_len, dst);
+  return hipGetLastError();
+}
+
+}  // namespace dfh

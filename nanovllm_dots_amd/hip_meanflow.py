@@ -1,0 +1,363 @@
+"""``fm_accel="hip"``: the MeanFlow FM/DiT head on hand-written gfx950 kernels.
+
+Drop-in callables for the reference's accelerator slots
+(nanovllm_dots/models/dots/engine.py:125-185, :615-633, :711-723):
+
+* ``HipMeanflow(core, num_steps=4, dit=None)`` — same constructor and
+  ``__call__`` signature as ``GraphedMeanflow`` (graphed_meanflow.py:26-60):
+  one whole solve per call, returns a fresh ``[N, P, latent_dim]`` bf16 tensor,
+  draws noise on the torch RNG outside the kernels when none is given, raises
+  ``RuntimeError`` on an NFE mismatch. Unlike the graph it replaces it never
+  captures, so a new (N, T) shape costs nothing beyond a workspace grow.
+* ``HipDiT(dit)`` — the per-forward ``vfp`` callable
+  (``vfp(*, x, timesteps, duration, attn_mask, pos_ids, g_cond) -> [B, T, ld]``,
+  batched_fm.py:120-121).
+* ``batched_meanflow(core, *, ..., vfp=None)`` — same signature as
+  batched_fm.py:82-93.
+
+Weights are read once from the DiT module's state dict (names of
+native/dit.py / native/layers.py) plus ``core.coordinate_proj``, and packed by
+the library (fused QKV, one adaLN matrix for every block).
+"""
+from __future__ import annotations
+
+import ctypes as C
+import math
+from dataclasses import dataclass
+
+import torch
+
+from . import _lib
+
+
+@dataclass
+class FMSpec:
+    """Shape of the DiT head (see include/dots_fm.h DfhConfig)."""
+    hidden: int
+    heads: int
+    ffn: int
+    n_blocks: int
+    latent_dim: int
+    patch: int
+    qkv_bias: bool = False
+    qk_norm: str = "none"       # "none" | "LayerNorm" | "RMSNorm"
+    rotary: bool = True
+    rotary_theta: float = 50000.0
+    freq_dim: int = 256
+    meanflow: bool = True
+    ln_eps: float = 1e-5
+
+    @property
+    def head_dim(self) -> int:
+        return self.hidden // self.heads
+
+    @classmethod
+    def of(cls, obj) -> "FMSpec":
+        """From any object with the same attribute names (duck-typed)."""
+        return cls(**{f: getattr(obj, f) for f in cls.__dataclass_fields__})
+
+    @classmethod
+    def from_modules(cls, dit, core) -> "FMSpec":
+        """From a reference DiT module (native/dit.py:111-133) and its core."""
+        blk = dit.blocks[0]
+        attn = blk.attn
+        qn = type(attn.q_norm).__name__
+        rot = bool(getattr(attn, "rotary_bias", False))
+        return cls(
+            hidden=dit.input_layer.out_features, heads=attn.num_heads,
+            ffn=blk.ffn.fc1.out_features, n_blocks=len(dit.blocks),
+            latent_dim=core.latent_dim, patch=core.latent_patch_size,
+            qkv_bias=attn.q_proj.bias is not None,
+            qk_norm={"Identity": "none"}.get(qn, qn), rotary=rot,
+            rotary_theta=float(getattr(attn.rotary, "_theta", 50000.0)) if rot else 50000.0,
+            freq_dim=dit.time_embedder.frequency_embedding_size,
+            meanflow=getattr(dit, "duration_embedder", None) is not None,
+            ln_eps=float(blk.norm1.eps))
+
+
+def rope_inv_freq(head_dim: int, theta: float) -> torch.Tensor:
+    """RotaryEmbedding.inv_freq (native/layers.py:110-113), float32 on the host."""
+    return 1.0 / (theta ** (torch.arange(0, head_dim, 2).float() / head_dim))
+
+
+def timestep_freqs(dim: int, max_period: float = 10000.0) -> torch.Tensor:
+    """TimestepEmbedder frequencies (native/dit.py:35-38), float32 on the host."""
+    half = dim // 2
+    return torch.exp(-math.log(max_period) * torch.arange(start=0, end=half, dtype=torch.float32) / half)
+
+
+def meanflow_grid(num_steps: int, dtype=torch.bfloat16):
+    """``linspace(0, 1, nfe+1)`` in the solver dtype and its bf16 step sizes
+    (batched_fm.py:113-116)."""
+    times = torch.linspace(0.0, 1.0, num_steps + 1, dtype=dtype)
+    ts = [float(times[s]) for s in range(num_steps)]
+    dts = [float(times[s + 1] - times[s]) for s in range(num_steps)]
+    return ts, dts
+
+
+_QKN = {"none": 0, "LayerNorm": 1, "RMSNorm": 2}
+
+
+class HipFMHead:
+    """Owns one library handle: packed weights + a growable workspace."""
+
+    def __init__(self, spec: FMSpec, weights: dict[str, torch.Tensor], device=None,
+                 inv_freq: torch.Tensor | None = None):
+        self.lib = _lib.lib()
+        self.spec = spec
+        self.device = torch.device(device if device is not None else "cuda")
+        s = spec
+        inv = (inv_freq.float().cpu() if inv_freq is not None
+               else rope_inv_freq(s.head_dim, s.rotary_theta)).contiguous()
+        tf = timestep_freqs(s.freq_dim).contiguous()
+        self._inv = (C.c_float * inv.numel())(*inv.tolist())
+        self._tf = (C.c_float * tf.numel())(*tf.tolist())
+        cfg = _lib.DfhConfig(
+            hidden=s.hidden, heads=s.heads, head_dim=s.head_dim, ffn=s.ffn, n_blocks=s.n_blocks,
+            latent_dim=s.latent_dim, patch=s.patch, freq_dim=s.freq_dim, qkv_bias=int(s.qkv_bias),
+            qk_norm=_QKN[s.qk_norm], rotary=int(s.rotary), meanflow=int(s.meanflow),
+            ln_eps=float(s.ln_eps), rope_inv_freq=C.cast(self._inv, C.POINTER(C.c_float)),
+            temb_freqs=C.cast(self._tf, C.POINTER(C.c_float)))
+        h = _lib.vp()
+        with torch.cuda.device(self.device):
+            _lib.check(self.lib.dfh_create(C.byref(cfg), C.byref(h)), "dfh_create")
+        self.handle = h
+        self.set_weights(weights)
+
+    # -- weights --------------------------------------------------------------
+    def set_weights(self, W: dict[str, torch.Tensor]) -> None:
+        s = self.spec
+        keep = []
+
+        def dev(name, required=True):
+            t = W.get(name)
+            if t is None:
+                if required:
+                    raise KeyError(f"missing DiT parameter {name!r}")
+                return None
+            t = t.detach().to(device=self.device, dtype=torch.bfloat16).contiguous()
+            keep.append(t)
+            return _lib.ptr(t)
+
+        blocks = (_lib.DfhBlockWeights * s.n_blocks)()
+        for l in range(s.n_blocks):
+            p = f"blocks.{l}."
+            b = blocks[l]
+            for nm in ("q", "k", "v"):
+                setattr(b, f"{nm}_w", dev(p + f"attn.{nm}_proj.weight"))
+                setattr(b, f"{nm}_b", dev(p + f"attn.{nm}_proj.bias", s.qkv_bias))
+            if s.qk_norm != "none":
+                b.q_norm_w = dev(p + "attn.q_norm.weight")
+                b.k_norm_w = dev(p + "attn.k_norm.weight")
+                if s.qk_norm == "LayerNorm":
+                    b.q_norm_b = dev(p + "attn.q_norm.bias")
+                    b.k_norm_b = dev(p + "attn.k_norm.bias")
+            b.o_w, b.o_b = dev(p + "attn.o_proj.weight"), dev(p + "attn.o_proj.bias")
+            b.fc1_w, b.fc1_b = dev(p + "ffn.fc1.weight"), dev(p + "ffn.fc1.bias")
+            b.fc2_w, b.fc2_b = dev(p + "ffn.fc2.weight"), dev(p + "ffn.fc2.bias")
+            b.ada_w = dev(p + "adaLN_modulation.1.weight")
+            b.ada_b = dev(p + "adaLN_modulation.1.bias")
+        w = _lib.DfhWeights(
+            input_w=dev("input_layer.weight"), input_b=dev("input_layer.bias"),
+            t_w0=dev("time_embedder.mlp.0.weight"), t_b0=dev("time_embedder.mlp.0.bias"),
+            t_w2=dev("time_embedder.mlp.2.weight"), t_b2=dev("time_embedder.mlp.2.bias"),
+            d_w0=dev("duration_embedder.mlp.0.weight", s.meanflow),
+            d_b0=dev("duration_embedder.mlp.0.bias", s.meanflow),
+            d_w2=dev("duration_embedder.mlp.2.weight", s.meanflow),
+            d_b2=dev("duration_embedder.mlp.2.bias", s.meanflow),
+            final_ada_w=dev("output_layer.adaLN_modulation.1.weight"),
+            final_ada_b=dev("output_layer.adaLN_modulation.1.bias"),
+            final_w=dev("output_layer.linear.weight"), final_b=dev("output_layer.linear.bias"),
+            coord_w=dev("coordinate_proj.weight"), coord_b=dev("coordinate_proj.bias"),
+            blocks=C.cast(blocks, C.POINTER(_lib.DfhBlockWeights)))
+        with torch.cuda.device(self.device):
+            _lib.check(self.lib.dfh_set_weights(self.handle, C.byref(w), _lib.stream_ptr()),
+                       "dfh_set_weights")
+        del keep
+
+    # -- entry points -----------------------------------------------------------
+    def solve(self, input_sequence, pos_ids, g_cond, noise, num_steps: int, *, strict=False):
+        s = self.spec
+        n, T, H = input_sequence.shape
+        self._check_inputs(input_sequence, pos_ids, g_cond)
+        if noise.shape != (n, s.patch, s.latent_dim):
+            raise RuntimeError(f"noise shape {tuple(noise.shape)} != {(n, s.patch, s.latent_dim)}")
+        inp = input_sequence.to(torch.bfloat16).contiguous()
+        pos = pos_ids.to(torch.float32).contiguous()
+        g = g_cond.to(torch.bfloat16).contiguous() if g_cond is not None else None
+        nz = noise.to(torch.bfloat16).contiguous()
+        out = torch.empty((n, s.patch, s.latent_dim), device=inp.device, dtype=torch.bfloat16)
+        ts, dts = meanflow_grid(num_steps)
+        tg = (C.c_float * num_steps)(*ts)
+        dg = (C.c_float * num_steps)(*dts)
+        args = _lib.DfhSolveArgs(n=n, total_len=T, num_steps=num_steps, input_sequence=_lib.ptr(inp),
+                                 pos_ids=_lib.ptr(pos), g_cond=_lib.ptr(g), noise=_lib.ptr(nz),
+                                 out=_lib.ptr(out), t_grid=tg, dt_grid=dg)
+        st = _lib.stream_ptr()
+        _lib.check(self.lib.dfh_meanflow_solve(self.handle, C.byref(args), st), "dfh_meanflow_solve")
+        if strict:
+            self._raise_input_status(st)
+        return out
+
+    def forward(self, x, timesteps, duration, pos_ids, g_cond, *, strict=False):
+        s = self.spec
+        n, T, H = x.shape
+        self._check_inputs(x, pos_ids, g_cond)
+        xx = x.to(torch.bfloat16).contiguous()
+        pos = pos_ids.to(torch.float32).contiguous()
+        g = g_cond.to(torch.bfloat16).contiguous() if g_cond is not None else None
+        tv = timesteps.reshape(-1).to(device=xx.device, dtype=torch.float32).expand(n).contiguous()
+        dv = None
+        if duration is not None and s.meanflow:
+            dv = duration.reshape(-1).to(device=xx.device, dtype=torch.float32).expand(n).contiguous()
+        out = torch.empty((n, T, s.latent_dim), device=xx.device, dtype=torch.bfloat16)
+        args = _lib.DfhForwardArgs(n=n, total_len=T, x=_lib.ptr(xx), timesteps=_lib.ptr(tv),
+                                   duration=_lib.ptr(dv), pos_ids=_lib.ptr(pos), g_cond=_lib.ptr(g),
+                                   out=_lib.ptr(out))
+        st = _lib.stream_ptr()
+        _lib.check(self.lib.dfh_dit_forward(self.handle, C.byref(args), st), "dfh_dit_forward")
+        if strict:
+            self._raise_input_status(st)
+        return out
+
+    def reserve(self, n: int, total_len: int, num_steps: int = 4) -> None:
+        _lib.check(self.lib.dfh_reserve(self.handle, n, total_len, num_steps, _lib.stream_ptr()),
+                   "dfh_reserve")
+
+    def profile(self, enable: bool) -> None:
+        _lib.check(self.lib.dfh_profile_enable(self.handle, int(enable)), "dfh_profile_enable")
+
+    PROFILE_CLASSES = ("qkv_gemm", "o_gemm", "fc1_gemm", "fc2_gemm", "attention", "ln_modulate", "other")
+
+    def profile_read(self) -> dict[str, tuple[float, int]]:
+        k = len(self.PROFILE_CLASSES)
+        ms = (C.c_double * k)()
+        cnt = (C.c_long * k)()
+        _lib.check(self.lib.dfh_profile_read(self.handle, ms, cnt, k), "dfh_profile_read")
+        return {name: (ms[i], cnt[i]) for i, name in enumerate(self.PROFILE_CLASSES)}
+
+    def close(self) -> None:
+        if getattr(self, "handle", None):
+            self.lib.dfh_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    # -- helpers ---------------------------------------------------------------
+    def _check_inputs(self, x, pos_ids, g_cond):
+        s = self.spec
+        if x.dim() != 3 or x.shape[2] != s.hidden:
+            raise RuntimeError(f"input must be [N, T, {s.hidden}], got {tuple(x.shape)}")
+        n, T, _ = x.shape
+        if not x.is_cuda:
+            raise RuntimeError("input must be on the GPU")
+        if T <= s.patch:
+            raise RuntimeError(f"total_len {T} must exceed the latent patch {s.patch}")
+        if pos_ids.shape != (n, T):
+            raise RuntimeError(f"pos_ids shape {tuple(pos_ids.shape)} != {(n, T)}")
+        if g_cond is not None and g_cond.reshape(n, -1).shape[1] != s.hidden:
+            raise RuntimeError("g_cond must be [N, hidden]")
+
+    def _raise_input_status(self, st):
+        flags = C.c_int(0)
+        _lib.check(self.lib.dfh_input_status(self.handle, C.byref(flags), st), "dfh_input_status")
+        if flags.value:
+            raise RuntimeError("pos_ids does not describe a valid FM layout "
+                               "(history length c = pos_ids[i, T-P] must be an integer in [1, T-P])")
+
+
+def _weights_from_modules(dit, core) -> dict[str, torch.Tensor]:
+    W = dict(dit.state_dict())
+    W["coordinate_proj.weight"] = core.coordinate_proj.weight
+    W["coordinate_proj.bias"] = core.coordinate_proj.bias
+    return W
+
+
+class HipMeanflow:
+    """Whole-solve MeanFlow on the HIP kernels; a drop-in for GraphedMeanflow."""
+
+    def __init__(self, core, *, num_steps: int = 4, dit=None, warmup: int = 0, head: HipFMHead = None,
+                 strict: bool = False):
+        self.core = core
+        self.nfe = num_steps
+        self.dit = dit if dit is not None else getattr(core, "velocity_field_predictor", None)
+        self.strict = strict
+        if head is None:
+            spec = FMSpec.from_modules(self.dit, core)
+            inv = None
+            if spec.rotary:
+                inv = self.dit.blocks[0].attn.rotary.inv_freq
+            head = HipFMHead(spec, _weights_from_modules(self.dit, core),
+                             device=next(self.dit.parameters()).device, inv_freq=inv)
+        self.head = head
+        self.latent_dim = head.spec.latent_dim
+        self.patch = head.spec.patch
+
+    @torch.no_grad()
+    def __call__(self, *, input_sequence, attn_mask, pos_ids, g_cond, num_steps=None, noise=None):
+        if num_steps is not None and num_steps != self.nfe:
+            raise RuntimeError(f"HipMeanflow built for nfe={self.nfe}, got {num_steps}.")
+        n = input_sequence.shape[0]
+        if noise is None:
+            noise = torch.randn((n, self.patch, self.latent_dim), device=input_sequence.device,
+                                dtype=input_sequence.dtype)
+        return self.head.solve(input_sequence, pos_ids, g_cond, noise, self.nfe, strict=self.strict)
+
+
+class HipDiT:
+    """The per-forward ``vfp`` callable: DiT.forward on the HIP kernels."""
+
+    def __init__(self, dit=None, core=None, *, head: HipFMHead = None, strict: bool = False):
+        if head is None:
+            spec = FMSpec.from_modules(dit, core)
+            inv = dit.blocks[0].attn.rotary.inv_freq if spec.rotary else None
+            head = HipFMHead(spec, _weights_from_modules(dit, core),
+                             device=next(dit.parameters()).device, inv_freq=inv)
+        self.head = head
+        self.strict = strict
+
+    @torch.no_grad()
+    def __call__(self, *, x, timesteps, duration=None, attn_mask=None, pos_ids=None, g_cond=None,
+                 **_kwargs):
+        if pos_ids is None:
+            raise RuntimeError("HipDiT needs pos_ids (the FM layout is read from them)")
+        return self.head.forward(x, timesteps, duration, pos_ids, g_cond, strict=self.strict)
+
+
+@torch.no_grad()
+def batched_meanflow(core, *, input_sequence, attn_mask, pos_ids, g_cond, num_steps: int = 4,
+                     noise=None, vfp=None):
+    """batched_fm.batched_meanflow with the HIP head. ``vfp=None`` runs the whole
+    solve in one library call (a HipMeanflow cached on ``core``); a ``HipDiT``
+    vfp runs the per-step loop of batched_fm.py:113-125 around it."""
+    n = input_sequence.size(0)
+    P = core.latent_patch_size
+    if noise is None:
+        noise = torch.randn((n, P, core.latent_dim), device=input_sequence.device,
+                            dtype=input_sequence.dtype)
+    if vfp is None:
+        mf = getattr(core, "_hip_meanflow", None)
+        if mf is None or mf.nfe != num_steps:
+            mf = HipMeanflow(core, num_steps=num_steps)
+            core._hip_meanflow = mf
+        return mf(input_sequence=input_sequence, attn_mask=attn_mask, pos_ids=pos_ids, g_cond=g_cond,
+                  num_steps=num_steps, noise=noise)
+    if not isinstance(vfp, HipDiT):
+        raise TypeError("batched_meanflow(fm_accel='hip') takes vfp=None or a HipDiT")
+    latent_start = input_sequence.size(1) - P
+    times = torch.linspace(0.0, 1.0, num_steps + 1, device=input_sequence.device,
+                           dtype=input_sequence.dtype)
+    z = noise
+    for step in range(num_steps):
+        t = times[step].expand(n)
+        dt = (times[step + 1] - times[step]).expand(n)
+        zp = core.coordinate_proj(z)
+        z_c = input_sequence.clone()
+        z_c[:, latent_start:] = zp
+        vt = vfp(x=z_c, timesteps=t, duration=dt, attn_mask=attn_mask, pos_ids=pos_ids, g_cond=g_cond)
+        z = z + vt[:, latent_start:] * dt.view(-1, 1, 1)
+    return z

@@ -1,0 +1,248 @@
+"""HIP path vs the oracle (CPU, bf16 regime) through the C ABI. GPU only.
+
+Tolerances: latents after the full NFE=4 solve must reach per-row cosine
+>= 0.9999 and max |diff| <= 0.02 * max |ref| against the oracle; the bf16
+GEMM's float32 output must match torch's fp32 matmul of the same bf16 operands
+to 1e-5 relative (accumulation order is the only difference)."""
+from __future__ import annotations
+
+import ctypes as C
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import cos_stats
+from oracle import dit_ref as R
+
+pytestmark = pytest.mark.gpu
+
+LAT_COS = 0.9999
+LAT_MAXABS_FRAC = 0.02
+
+
+def _head(cfg, seed=0):
+    from nanovllm_dots_amd import FMSpec, HipFMHead
+    W = R.random_dit_weights(cfg, seed)
+    head = HipFMHead(FMSpec.of(cfg), W, device="cuda")
+    return head, R.weights_for_regime(W, "bf16")
+
+
+def _inputs(cfg, n, lo, hi, seed):
+    lens, hist, noise = R.synthetic_requests(n, lo, hi, cfg, seed)
+    inp, mask, pos, g = R.pack_fm_inputs(hist, cfg.patch, cfg.hidden)
+    return lens, hist, noise, inp, mask, pos, g
+
+
+def _cuda_bf16(t):
+    return t.to(device="cuda", dtype=torch.bfloat16).contiguous()
+
+
+def _assert_latents(got, ref, ld, label):
+    got, ref = got.float().cpu(), ref.float().cpu()
+    cmin, cmean = cos_stats(got, ref, ld)
+    err = (got - ref).abs().max().item()
+    scale = ref.abs().max().item()
+    print(f"{label}: cos min {cmin:.6f} mean {cmean:.6f} maxabs {err:.4g} (|ref| {scale:.3g})", flush=True)
+    assert cmin >= LAT_COS, f"{label}: cos min {cmin:.6f}"
+    assert err <= LAT_MAXABS_FRAC * scale, f"{label}: max abs {err}"
+
+
+# ----------------------------------------------------------------------------- GEMM
+GEMM_CASES = [(1, 64, 64, 3), (37, 128, 256, 2), (300, 1024, 1024, -1), (700, 1024, 1024, 0),
+              (1000, 3072, 1024, 1), (513, 1024, 4096, -1), (64, 75776 // 8, 1024, -1)]
+
+
+@pytest.mark.parametrize("M,N,K,tile", GEMM_CASES)
+def test_gemm_f32_out_matches_torch(M, N, K, tile):
+    from nanovllm_dots_amd import _lib
+    lib = _lib.lib()
+    g = torch.Generator(device="cpu").manual_seed(M * 7 + N)
+    A = torch.randn(M, K, generator=g).bfloat16().cuda()
+    B = (0.05 * torch.randn(N, K, generator=g)).bfloat16().cuda()
+    bias = (0.1 * torch.randn(N, generator=g)).bfloat16().cuda()
+    out = torch.empty(M, N, device="cuda", dtype=torch.float32)
+    print(f"gemm M={M} N={N} K={K} tile={tile}", flush=True)
+    _lib.check(lib.dfh_gemm_bf16(_lib.ptr(A), K, _lib.ptr(B), K, _lib.ptr(out), N, _lib.ptr(bias),
+                                 M, N, K, 4, tile, _lib.stream_ptr()))
+    ref = A.float() @ B.float().t() + bias.float()
+    torch.cuda.synchronize()
+    rel = ((out - ref).abs().max() / ref.abs().max()).item()
+    assert rel < 1e-5, rel
+
+
+@pytest.mark.parametrize("epi", [0, 1])
+def test_gemm_bf16_epilogues(epi):
+    from nanovllm_dots_amd import _lib
+    lib = _lib.lib()
+    M, N, K = 333, 512, 1024
+    g = torch.Generator(device="cpu").manual_seed(epi)
+    A = torch.randn(M, K, generator=g).bfloat16().cuda()
+    B = (0.03 * torch.randn(N, K, generator=g)).bfloat16().cuda()
+    bias = (0.1 * torch.randn(N, generator=g)).bfloat16().cuda()
+    out = torch.empty(M, N, device="cuda", dtype=torch.bfloat16)
+    _lib.check(lib.dfh_gemm_bf16(_lib.ptr(A), K, _lib.ptr(B), K, _lib.ptr(out), N, _lib.ptr(bias),
+                                 M, N, K, epi, -1, _lib.stream_ptr()))
+    pre = (A.float() @ B.float().t() + bias.float()).bfloat16().float()
+    ref = pre
+    if epi == 1:
+        ref = torch.nn.functional.gelu(pre, approximate="tanh").bfloat16().float()
+    torch.cuda.synchronize()
+    diff = (out.float() - ref).abs()
+    # the pre-activation may differ by one bf16 ulp (accumulation order); GELU's
+    # slope is within [-0.2, 1.2], then one more output rounding
+    tol = pre.abs() * 2 ** -7 * (1.2 if epi == 1 else 1.0) + ref.abs() * 2 ** -8 + 1e-6
+    assert (diff <= tol).all(), diff.max()
+
+
+# ----------------------------------------------------------------------------- DiT / solve
+SMALL = dict(hidden=256, heads=4, ffn=1024, n_blocks=2, latent_dim=64, patch=16)
+VARIANTS = {
+    "rope": R.DitConfig(**SMALL),
+    "qknorm_bias": R.DitConfig(**SMALL, qkv_bias=True, qk_norm="LayerNorm"),
+    "rms_norope": R.DitConfig(**SMALL, qk_norm="RMSNorm", rotary=False),
+}
+
+
+@pytest.mark.parametrize("name", list(VARIANTS))
+def test_dit_forward_matches_oracle(name):
+    from nanovllm_dots_amd import HipDiT
+    cfg = VARIANTS[name]
+    head, Wb = _head(cfg, seed=3)
+    lens, hist, noise, inp, mask, pos, g = _inputs(cfg, 3, 1, 150, seed=5)
+    n, T = inp.shape[0], inp.shape[1]
+    rs = np.random.RandomState(9)
+    x = inp.clone()
+    x[:, T - cfg.patch:] = R.round_bf16(torch.from_numpy(rs.standard_normal((n, cfg.patch, cfg.hidden)).astype(np.float32)))
+    t = R.round_bf16(torch.from_numpy(rs.uniform(0, 1, n).astype(np.float32)))
+    dur = R.round_bf16(torch.from_numpy(rs.uniform(0, 1, n).astype(np.float32)))
+    gc = R.round_bf16(torch.from_numpy(0.5 * rs.standard_normal((n, cfg.hidden)).astype(np.float32)))
+    print(f"dit_forward {name} lens={lens}", flush=True)
+    ref = R.dit_forward(Wb, cfg, x, t, dur, mask, pos, gc, regime="bf16")
+    got = HipDiT(head=head, strict=True)(x=_cuda_bf16(x), timesteps=t.cuda(), duration=dur.cuda(),
+                                         attn_mask=None, pos_ids=pos.cuda(), g_cond=_cuda_bf16(gc))
+    got = got.float().cpu()
+    for i, L in enumerate(lens):
+        rows = list(range(L)) + list(range(T - cfg.patch, T))
+        cmin, _ = cos_stats(got[i, rows], ref[i, rows])
+        assert cmin >= LAT_COS, (i, L, cmin)
+        pad = [r for r in range(T) if r not in rows]
+        assert torch.all(got[i, pad] == 0)
+
+
+@pytest.mark.parametrize("name", list(VARIANTS))
+def test_meanflow_solve_matches_oracle(name):
+    from nanovllm_dots_amd import HipMeanflow
+    cfg = VARIANTS[name]
+    head, Wb = _head(cfg, seed=4)
+    lens, hist, noise, inp, mask, pos, g = _inputs(cfg, 4, 1, 200, seed=6)
+    print(f"meanflow {name} lens={lens}", flush=True)
+    ref = R.meanflow_solve(Wb, cfg, inp, mask, pos, g, noise, 4, "bf16")
+    mf = HipMeanflow(None, num_steps=4, dit=object(), head=head, strict=True)
+    got = mf(input_sequence=_cuda_bf16(inp), attn_mask=mask.cuda(), pos_ids=pos.cuda(),
+             g_cond=_cuda_bf16(g), noise=_cuda_bf16(noise))
+    _assert_latents(got, ref, cfg.latent_dim, f"meanflow-{name}")
+
+
+def test_padding_transparency_bit_exact():
+    """A ragged batch gives each request bit-identical latents to a solo run."""
+    from nanovllm_dots_amd import HipMeanflow
+    cfg = VARIANTS["rope"]
+    head, _ = _head(cfg, seed=7)
+    mf = HipMeanflow(None, num_steps=4, dit=object(), head=head)
+    lens, hist, noise, inp, mask, pos, g = _inputs(cfg, 5, 1, 180, seed=8)
+    batched = mf(input_sequence=_cuda_bf16(inp), attn_mask=None, pos_ids=pos.cuda(),
+                 g_cond=_cuda_bf16(g), noise=_cuda_bf16(noise))
+    for i in range(5):
+        i1, m1, p1, g1 = R.pack_fm_inputs([hist[i]], cfg.patch, cfg.hidden)
+        solo = mf(input_sequence=_cuda_bf16(i1), attn_mask=None, pos_ids=p1.cuda(), g_cond=_cuda_bf16(g1),
+                  noise=_cuda_bf16(noise[i:i + 1]))
+        assert torch.equal(solo[0], batched[i]), i
+
+
+def test_shape_changes_without_recapture_and_shrink():
+    """Successive calls with different (N, T) — growing and shrinking — each
+    match the oracle; nothing is captured."""
+    from nanovllm_dots_amd import HipMeanflow
+    cfg = VARIANTS["rope"]
+    head, Wb = _head(cfg, seed=11)
+    mf = HipMeanflow(None, num_steps=4, dit=object(), head=head, strict=True)
+    for k, (n, lo, hi) in enumerate([(2, 3, 30), (6, 50, 260), (1, 1, 1), (3, 10, 90)]):
+        lens, hist, noise, inp, mask, pos, g = _inputs(cfg, n, lo, hi, seed=20 + k)
+        ref = R.meanflow_solve(Wb, cfg, inp, mask, pos, g, noise, 4, "bf16")
+        got = mf(input_sequence=_cuda_bf16(inp), attn_mask=None, pos_ids=pos.cuda(),
+                 g_cond=_cuda_bf16(g), noise=_cuda_bf16(noise))
+        _assert_latents(got, ref, cfg.latent_dim, f"shape{k} n={n}")
+
+
+def test_nfe_mismatch_and_bad_layout_raise():
+    from nanovllm_dots_amd import HipMeanflow
+    cfg = VARIANTS["rope"]
+    head, _ = _head(cfg, seed=1)
+    mf = HipMeanflow(None, num_steps=4, dit=object(), head=head, strict=True)
+    lens, hist, noise, inp, mask, pos, g = _inputs(cfg, 2, 5, 9, seed=1)
+    with pytest.raises(RuntimeError, match="nfe"):
+        mf(input_sequence=_cuda_bf16(inp), attn_mask=None, pos_ids=pos.cuda(), g_cond=None,
+           num_steps=3, noise=_cuda_bf16(noise))
+    bad = pos.clone()
+    bad[0, -cfg.patch] = 0.0   # history length 0 is not a valid FM layout
+    with pytest.raises(RuntimeError, match="valid FM layout"):
+        mf(input_sequence=_cuda_bf16(inp), attn_mask=None, pos_ids=bad.cuda(), g_cond=None,
+           noise=_cuda_bf16(noise))
+    # the handle stays usable after a rejected input
+    out = mf(input_sequence=_cuda_bf16(inp), attn_mask=None, pos_ids=pos.cuda(), g_cond=None,
+             noise=_cuda_bf16(noise))
+    assert torch.isfinite(out.float()).all()
+
+
+def test_noise_drawn_from_torch_rng_when_absent():
+    from nanovllm_dots_amd import HipMeanflow
+    cfg = VARIANTS["rope"]
+    head, _ = _head(cfg, seed=2)
+    mf = HipMeanflow(None, num_steps=4, dit=object(), head=head)
+    lens, hist, noise, inp, mask, pos, g = _inputs(cfg, 2, 5, 40, seed=2)
+    torch.manual_seed(123)
+    a = mf(input_sequence=_cuda_bf16(inp), attn_mask=None, pos_ids=pos.cuda(), g_cond=None)
+    torch.manual_seed(123)
+    nz = torch.randn((2, cfg.patch, cfg.latent_dim), device="cuda", dtype=torch.bfloat16)
+    b = mf(input_sequence=_cuda_bf16(inp), attn_mask=None, pos_ids=pos.cuda(), g_cond=None, noise=nz)
+    assert torch.equal(a, b)
+
+
+# ----------------------------------------------------------------------------- full size
+FULL = R.DitConfig(hidden=1024, heads=16, ffn=4096, n_blocks=12, latent_dim=64, patch=16)
+
+
+def test_full_size_one_step_forward_c2():
+    """8 requests, contexts U{64..512} projected from 1536-d N(0,1) states, one
+    DiT forward at t=0, dt=0.25 (12 blocks, H=1024)."""
+    from nanovllm_dots_amd import HipDiT
+    cfg = FULL
+    head, Wb = _head(cfg, seed=0)
+    lens, hist, noise = R.synthetic_requests(8, 64, 512, cfg, seed=0, llm_width=1536)
+    inp, mask, pos, g = R.pack_fm_inputs(hist, cfg.patch, cfg.hidden)
+    n, T = inp.shape[:2]
+    zp = R._R("bf16").linear(noise, Wb["coordinate_proj.weight"], Wb["coordinate_proj.bias"])
+    x = inp.clone()
+    x[:, T - cfg.patch:] = zp
+    t = torch.zeros(n)
+    dt = torch.full((n,), 0.25)
+    print(f"c2 forward lens={lens}", flush=True)
+    ref = R.dit_forward(Wb, cfg, x, t, dt, mask, pos, g, regime="bf16")[:, T - cfg.patch:]
+    got = HipDiT(head=head)(x=_cuda_bf16(x), timesteps=t.cuda(), duration=dt.cuda(), pos_ids=pos.cuda(),
+                            g_cond=_cuda_bf16(g))[:, T - cfg.patch:]
+    _assert_latents(got, ref, cfg.latent_dim, "c2-forward")
+
+
+def test_full_size_nfe4_solve():
+    """Full 12-block NFE=4 solve, 4 requests with contexts U{64..384}."""
+    from nanovllm_dots_amd import HipMeanflow
+    cfg = FULL
+    head, Wb = _head(cfg, seed=1)
+    lens, hist, noise, inp, mask, pos, g = _inputs(cfg, 4, 64, 384, seed=3)
+    print(f"full solve lens={lens}", flush=True)
+    ref = R.meanflow_solve_varlen(Wb, cfg, hist, g, noise, 4, "bf16")
+    mf = HipMeanflow(None, num_steps=4, dit=object(), head=head, strict=True)
+    got = mf(input_sequence=_cuda_bf16(inp), attn_mask=None, pos_ids=pos.cuda(), g_cond=_cuda_bf16(g),
+             noise=_cuda_bf16(noise))
+    _assert_latents(got, ref, cfg.latent_dim, "full-nfe4")
