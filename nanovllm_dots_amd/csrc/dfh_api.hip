@@ -138,6 +138,19 @@ hipError_t gemm(DfhHandle* h, int pc, const GemmArgs& a, int epi, hipStream_t s,
   return gemm_bf16(a, epi, s, tile);
 }
 
+// Tile shape per GEMM role (indices of gemm_bf16's configurations), chosen from
+// measured throughput at M ~ 37k rows: 8-wave 256x256 for the wide (N=4096) and the
+// deep (K=4096) products, two 128x256 workgroups per CU for N=1024, K=1024 (their
+// epilogues overlap the other workgroup's MFMAs), 128x128 for the fused QKV.
+enum GemmRole { kRoleQKV, kRoleNarrow, kRoleWide };
+int tile_for(long M, int N, int K, GemmRole role) {
+  if (M < 4096) return -1;  // small problems: the library heuristic
+  if (role == kRoleQKV) return 2;
+  if (role == kRoleWide) return N % 256 == 0 ? 0 : -1;
+  if (K >= 4096 && N % 256 == 0) return 0;
+  return (N % 256 == 0 && K % 32 == 0) ? 5 : -1;
+}
+
 GemmArgs linear_args(const uint16_t* A, long lda, const uint16_t* W, const uint16_t* b, uint16_t* C,
                      long ldc, int M, const int* M_dev, int N, int K) {
   GemmArgs a;
@@ -247,7 +260,8 @@ int dit_blocks(DfhHandle* h, int n, int T, long mod_row0, hipStream_t s) {
 
   // input_layer
   DFH_CHECK(gemm(h, PC_OTHER, linear_args(P<uint16_t>(h->seq), H, h->in_w, h->in_b,
-                                          P<uint16_t>(h->x), H, Mup, Md, H, H), EPI_BIAS, s));
+                                          P<uint16_t>(h->x), H, Mup, Md, H, H), EPI_BIAS, s,
+                 tile_for(Mup, H, H, kRoleNarrow)));
   for (int l = 0; l < c.n_blocks; ++l) {
     const uint16_t* ml = mod + (long)l * 6 * H;  // shift_a, scale_a, gate_a, shift_f, scale_f, gate_f
     prof_arm(h, PC_LN);
@@ -262,7 +276,7 @@ int dit_blocks(DfhHandle* h, int n, int T, long mod_row0, hipStream_t s) {
     q.qk_norm = c.qk_norm;
     q.qn_w = h->qn_w[l]; q.qn_b = h->qn_b[l]; q.kn_w = h->kn_w[l]; q.kn_b = h->kn_b[l];
     q.vt = P<uint16_t>(h->vt); q.ld_vt = h->ld_vt; q.vt_col = P<int>(h->vt_col);
-    DFH_CHECK(gemm(h, PC_QKV, q, EPI_QKV, s, 1));
+    DFH_CHECK(gemm(h, PC_QKV, q, EPI_QKV, s, tile_for(Mup, 3 * H, H, kRoleQKV)));
     prof_arm(h, PC_ATTN);
     DFH_CHECK(fm_attention(P<uint16_t>(h->qk), 2 * H, P<uint16_t>(h->vt), h->ld_vt,
                            P<uint16_t>(h->attn), H, P<int>(h->cu_rows), P<int>(h->cu_vt),
@@ -270,16 +284,17 @@ int dit_blocks(DfhHandle* h, int n, int T, long mod_row0, hipStream_t s) {
     GemmArgs o = linear_args(P<uint16_t>(h->attn), H, h->o_w[l], h->o_b[l], P<uint16_t>(h->x), H,
                              Mup, Md, H, H);
     o.gate = ml + 2 * H; o.ld_gate = ldm; o.row_req = row_req;
-    DFH_CHECK(gemm(h, PC_O, o, EPI_GATE_RES, s));
+    DFH_CHECK(gemm(h, PC_O, o, EPI_GATE_RES, s, tile_for(Mup, H, H, kRoleNarrow)));
     prof_arm(h, PC_LN);
     DFH_CHECK(ln_modulate(P<uint16_t>(h->x), H, P<uint16_t>(h->hbuf), H, ml + 3 * H, ml + 4 * H, ldm,
                           row_req, nullptr, Mup, Md, H, c.ln_eps, s));
     DFH_CHECK(gemm(h, PC_FC1, linear_args(P<uint16_t>(h->hbuf), H, h->fc1_w[l], h->fc1_b[l],
-                                          P<uint16_t>(h->ff), F, Mup, Md, F, H), EPI_GELU, s));
+                                          P<uint16_t>(h->ff), F, Mup, Md, F, H), EPI_GELU, s,
+                   tile_for(Mup, F, H, kRoleWide)));
     GemmArgs f2 = linear_args(P<uint16_t>(h->ff), F, h->fc2_w[l], h->fc2_b[l], P<uint16_t>(h->x), H,
                               Mup, Md, H, F);
     f2.gate = ml + 5 * H; f2.ld_gate = ldm; f2.row_req = row_req;
-    DFH_CHECK(gemm(h, PC_FC2, f2, EPI_GATE_RES, s));
+    DFH_CHECK(gemm(h, PC_FC2, f2, EPI_GATE_RES, s, tile_for(Mup, H, F, kRoleNarrow)));
   }
   return 0;
 }

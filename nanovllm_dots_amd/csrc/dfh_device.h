@@ -15,24 +15,28 @@ typedef int intx16 __attribute__((ext_vector_type(16)));
 
 __device__ __forceinline__ float bf2f(bf16_t h) { return __uint_as_float(((uint32_t)h) << 16); }
 
-// float -> bf16, round to nearest even (NaN kept quiet).
-__device__ __forceinline__ bf16_t f2bf(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (bf16_t)((u >> 16) | 0x40u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return (bf16_t)(u >> 16);
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float floatx2_t __attribute__((ext_vector_type(2)));
+
+// float -> bf16, round to nearest even (v_cvt_pk_bf16_f32; NaN stays NaN).
+__device__ __forceinline__ bf16_t f2bf(float f) { return __builtin_bit_cast(bf16_t, (__bf16)f); }
+
+// two floats -> packed bf16 pair (low half = a), one v_cvt_pk_bf16_f32
+__device__ __forceinline__ uint32_t pack2(float a, float b) {
+  floatx2_t v = {a, b};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
 }
 
 // round a float to the nearest bf16 value, returned as float
-__device__ __forceinline__ float rbf(float f) { return bf2f(f2bf(f)); }
+__device__ __forceinline__ float rbf(float f) { return (float)(__bf16)f; }
 
 struct alignas(8) bf16q { bf16_t v[4]; };
 struct alignas(16) bf16o { bf16_t v[8]; };
 
 __device__ __forceinline__ uint2 pack4(float a, float b, float c, float d) {
   uint2 r;
-  r.x = (uint32_t)f2bf(a) | ((uint32_t)f2bf(b) << 16);
-  r.y = (uint32_t)f2bf(c) | ((uint32_t)f2bf(d) << 16);
+  r.x = pack2(a, b);
+  r.y = pack2(c, d);
   return r;
 }
 
@@ -43,12 +47,15 @@ __device__ __forceinline__ void unpack4(uint2 r, float* o) {
   o[3] = bf2f((bf16_t)(r.y >> 16));
 }
 
-// GELU, tanh approximation: 0.5*x*(1+tanh(sqrt(2/pi)*(x+0.044715x^3))), fp32.
+// GELU, tanh approximation: 0.5*x*(1+tanh(u)), u = sqrt(2/pi)*(x+0.044715x^3), fp32.
+// Evaluated as x * sigmoid(2u) = x / (1 + 2^(-2u*log2(e))): the same function
+// (0.5*(1+tanh(u)) == sigmoid(2u)) with one exp2 and one reciprocal.
 __device__ __forceinline__ float gelu_tanh_f(float x) {
-  const float k0 = 0.7978845608028654f, k1 = 0.044715f;
-  float x3 = x * x * x;
-  float inner = k0 * (x + k1 * x3);
-  return 0.5f * x * (1.0f + tanhf(inner));
+  // -2*log2(e)*sqrt(2/pi) and its product with 0.044715
+  const float c1 = -2.0f * 1.4426950408889634f * 0.7978845608028654f;
+  const float c2 = c1 * 0.044715f;
+  const float z = x * __builtin_fmaf(c2, x * x, c1);  // -2*log2(e)*u
+  return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(z));
 }
 
 __device__ __forceinline__ float silu_f(float x) { return x / (1.0f + expf(-x)); }

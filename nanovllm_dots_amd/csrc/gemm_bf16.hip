@@ -10,9 +10,15 @@
 // coalesced column writes of V^T.
 //
 // Schedule: persistent workgroups (grid = resident WGs), tiles walked in
-// XCD-contiguous chunks so the row tiles that share A live in one XCD's L2,
-// LDS double buffering with one barrier per 64-wide K step, global loads for
-// step k+1 issued before the MFMAs of step k.
+// XCD-contiguous chunks so the row tiles that share A live in one XCD's L2.
+// Operands move global -> LDS by DMA (global_load_lds_dwordx4: no staging
+// registers, no ds_write) into ST statically distinct LDS stages: the DMA of K
+// step k+ST-1 is issued while step k computes. Each step starts with an
+// explicit wait for this wave's own DMA of step k (vmcnt) plus its LDS reads
+// (lgkmcnt), then a barrier, so the step's tile is complete for every wave and
+// the stage refilled next is no longer read by anyone.
+#include <type_traits>
+
 #include "dfh_device.h"
 #include "dfh_kernels.h"
 
@@ -20,174 +26,59 @@ namespace dfh {
 
 namespace {
 
-constexpr int BK = 64;
-constexpr int LDK = BK + 8;  // padded LDS row (elements): 144 B keeps 16-B reads conflict-free
+#define DFH_GPTR(p) ((__attribute__((address_space(1))) void*)(p))
+#define DFH_LPTR(p) ((__attribute__((address_space(3))) void*)(p))
 
-template <int BM, int BN, int WM, int WN>
+template <int BM_, int BN_, int BK_, int ST_, int WM_, int WN_>
 struct Cfg {
+  static constexpr int BM = BM_, BN = BN_, BK = BK_, ST = ST_, WM = WM_, WN = WN_;
   static constexpr int THREADS = 64 * WM * WN;
+  static constexpr int NW = WM * WN;
   static constexpr int WTM = BM / WM;  // wave tile rows (activations)
   static constexpr int WTN = BN / WN;  // wave tile cols (outputs)
   static constexpr int RM = WTM / 32;
   static constexpr int RN = WTN / 32;
-  static constexpr int A_CHUNKS = BM * BK / 8 / THREADS;  // 16-B chunks per thread per K step
-  static constexpr int B_CHUNKS = BN * BK / 8 / THREADS;
-  static constexpr int LDS_BYTES = 2 * (BM + BN) * LDK * 2;
+  static constexpr int CH = BK / 8;                 // 16-B chunks per LDS row
+  static constexpr int ROWS_PER_DMA = 64 / CH;      // rows one wave fills per DMA (1 KB)
+  static constexpr int RPR = NW * ROWS_PER_DMA;     // rows per DMA round of the workgroup
+  static constexpr int AJ = BM / RPR, BJ = BN / RPR;
+  static constexpr int LPS = AJ + BJ;               // DMA instructions per wave per K step
+  static constexpr int LDS_BYTES = ST * (BM + BN) * BK * 2;
+  // two workgroups per CU when both fit in LDS (then <= 256 registers per lane)
+  static constexpr int WG_PER_CU = (NW <= 4 && 2 * LDS_BYTES <= 160 * 1024) ? 2 : 1;
+  static constexpr int WAVES_PER_EU = WG_PER_CU * NW / 4;
   static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tile");
-  static_assert((BM * BK / 8) % THREADS == 0 && (BN * BK / 8) % THREADS == 0, "load split");
+  static_assert(BM % RPR == 0 && BN % RPR == 0, "DMA rounds");
+  static_assert(BK == 32 || BK == 64, "BK");
+  static_assert(ST >= 1 && ST <= 4, "stages");
 };
 
-template <int EPI>
-__device__ __forceinline__ void epilogue_store4(const GemmArgs& a, int m, int n, const float* v4) {
-  // v4: 4 accumulators for columns n..n+3 of row m (m < M checked by caller)
-  float y[4];
-  if (a.bias) {
-    uint2 bb = *reinterpret_cast<const uint2*>(a.bias + n);
-    float b[4];
-    unpack4(bb, b);
-#pragma unroll
-    for (int t = 0; t < 4; ++t) y[t] = v4[t] + b[t];
-  } else {
-#pragma unroll
-    for (int t = 0; t < 4; ++t) y[t] = v4[t];
-  }
-  if constexpr (EPI == EPI_F32) {
-    float4 o = make_float4(y[0], y[1], y[2], y[3]);
-    *reinterpret_cast<float4*>(a.Cf + (long)m * a.ldc + n) = o;
-    return;
-  }
-#pragma unroll
-  for (int t = 0; t < 4; ++t) y[t] = rbf(y[t]);
-  if constexpr (EPI == EPI_GELU) {
-#pragma unroll
-    for (int t = 0; t < 4; ++t) y[t] = gelu_tanh_f(y[t]);
-  }
-  if constexpr (EPI == EPI_GATE_RES) {
-    const int req = a.row_req[m];
-    float g[4], x[4];
-    unpack4(*reinterpret_cast<const uint2*>(a.gate + (long)req * a.ld_gate + n), g);
-    uint16_t* cp = a.C + (long)m * a.ldc + n;
-    unpack4(*reinterpret_cast<const uint2*>(cp), x);
-#pragma unroll
-    for (int t = 0; t < 4; ++t) y[t] = x[t] + rbf(g[t] * y[t]);
-  }
-  *reinterpret_cast<uint2*>(a.C + (long)m * a.ldc + n) = pack4(y[0], y[1], y[2], y[3]);
+// LDS tile layout: rows of BK bf16 (BK/8 16-B chunks), row-major, logical chunk
+// c of row r at slot c ^ swz(r). The LDS serves a ds_read_b128 sixteen lanes
+// (256 B, 64 banks) at a time; a fragment read gives those lanes 16 consecutive
+// rows at one logical chunk and the swizzle makes their 16-B bank groups
+// (row, slot) -> (row*CH + slot) % 16 all distinct.
+template <int CH>
+__device__ __forceinline__ int swz(int row) {
+  return CH == 8 ? ((row >> 1) & 7) : ((row >> 2) & 3);
+}
+template <int CH>
+__device__ __forceinline__ int lds_off(int row, int chunk) {
+  return row * (CH * 8) + ((chunk ^ swz<CH>(row)) << 3);
 }
 
-template <int BM, int BN, int WM, int WN, int EPI>
-__global__ void __launch_bounds__(64 * WM * WN, 1)
-gemm_bf16_kernel(GemmArgs a) {
-  using C = Cfg<BM, BN, WM, WN>;
-  extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
-  uint16_t* As = smem;                       // [2][BM][LDK]
-  uint16_t* Bs = smem + 2 * BM * LDK;        // [2][BN][LDK]
+// s_waitcnt vmcnt(n) lgkmcnt(0) (gfx9 encoding: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt_hi[15:14])
+template <int N>
+__device__ __forceinline__ void wait_vm_lgkm0() {
+  static_assert(N >= 0 && N < 64, "vmcnt");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (0 << 8) | ((N >> 4) << 14));
+}
 
-  const int M = a.M_dev ? *a.M_dev : a.M;
-  const int N = a.N, K = a.K;
-  const int tiles_m = (M + BM - 1) / BM;
-  const int tiles_n = N / BN;
-  const int total = tiles_m * tiles_n;
-  if (total == 0) return;
 
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const int wm = wave / WN, wn = wave % WN;
-  const int l32 = lane & 31, hi = lane >> 5;
 
-  // XCD-contiguous tile walk: workgroups with equal blockIdx.x % 8 share an XCD.
-  const int nxcd = 8;
-  const int xcd = blockIdx.x % nxcd;
-  const int slot = blockIdx.x / nxcd;
-  const int per_xcd = gridDim.x / nxcd;
-  const int chunk = (total + nxcd - 1) / nxcd;
-
-  for (int j = slot; j < chunk; j += per_xcd) {
-    const int tile = xcd * chunk + j;
-    if (tile >= total) break;
-    const int tm = tile / tiles_n, tn = tile % tiles_n;
-    const int m0 = tm * BM, n0 = tn * BN;
-
-    // per-thread global chunk offsets in elements (fixed over K; rows past M clamp to M-1)
-    int a_off[C::A_CHUNKS], a_lds[C::A_CHUNKS];
-#pragma unroll
-    for (int c = 0; c < C::A_CHUNKS; ++c) {
-      int idx = tid + c * C::THREADS;
-      int row = idx >> 3, col = (idx & 7) * 8;
-      int gm = m0 + row;
-      gm = gm < M ? gm : M - 1;
-      a_off[c] = gm * (int)a.lda + col;
-      a_lds[c] = row * LDK + col;
-    }
-    int b_off[C::B_CHUNKS], b_lds[C::B_CHUNKS];
-#pragma unroll
-    for (int c = 0; c < C::B_CHUNKS; ++c) {
-      int idx = tid + c * C::THREADS;
-      int row = idx >> 3, col = (idx & 7) * 8;
-      b_off[c] = (n0 + row) * (int)a.ldb + col;
-      b_lds[c] = row * LDK + col;
-    }
-
-    floatx16 acc[C::RN][C::RM];
-#pragma unroll
-    for (int i = 0; i < C::RN; ++i)
-#pragma unroll
-      for (int k = 0; k < C::RM; ++k)
-#pragma unroll
-        for (int t = 0; t < 16; ++t) acc[i][k][t] = 0.f;
-
-    uint4 ra[C::A_CHUNKS], rb[C::B_CHUNKS];
-#pragma unroll
-    for (int c = 0; c < C::A_CHUNKS; ++c) ra[c] = *reinterpret_cast<const uint4*>(a.A + a_off[c]);
-#pragma unroll
-    for (int c = 0; c < C::B_CHUNKS; ++c) rb[c] = *reinterpret_cast<const uint4*>(a.B + b_off[c]);
-    __syncthreads();  // previous tile's LDS readers are done
-#pragma unroll
-    for (int c = 0; c < C::A_CHUNKS; ++c) *reinterpret_cast<uint4*>(As + a_lds[c]) = ra[c];
-#pragma unroll
-    for (int c = 0; c < C::B_CHUNKS; ++c) *reinterpret_cast<uint4*>(Bs + b_lds[c]) = rb[c];
-    __syncthreads();
-
-    const int KT = K / BK;
-    for (int kt = 0; kt < KT; ++kt) {
-      const int cur = kt & 1;
-      if (kt + 1 < KT) {
-        const int koff = (kt + 1) * BK;
-#pragma unroll
-        for (int c = 0; c < C::A_CHUNKS; ++c) ra[c] = *reinterpret_cast<const uint4*>(a.A + a_off[c] + koff);
-#pragma unroll
-        for (int c = 0; c < C::B_CHUNKS; ++c) rb[c] = *reinterpret_cast<const uint4*>(a.B + b_off[c] + koff);
-      }
-      const uint16_t* as = As + cur * BM * LDK + (wm * C::WTM + l32) * LDK + hi * 8;
-      const uint16_t* bs = Bs + cur * BN * LDK + (wn * C::WTN + l32) * LDK + hi * 8;
-#pragma unroll
-      for (int kk = 0; kk < BK / 16; ++kk) {
-        bf16x8 fa[C::RM], fb[C::RN];
-#pragma unroll
-        for (int i = 0; i < C::RM; ++i)
-          fa[i] = *reinterpret_cast<const bf16x8*>(as + i * 32 * LDK + kk * 16);
-#pragma unroll
-        for (int i = 0; i < C::RN; ++i)
-          fb[i] = *reinterpret_cast<const bf16x8*>(bs + i * 32 * LDK + kk * 16);
-#pragma unroll
-        for (int i = 0; i < C::RN; ++i)
-#pragma unroll
-          for (int k = 0; k < C::RM; ++k)
-            acc[i][k] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[i], fa[k], acc[i][k], 0, 0, 0);
-      }
-      if (kt + 1 < KT) {
-        const int nxt = cur ^ 1;
-#pragma unroll
-        for (int c = 0; c < C::A_CHUNKS; ++c)
-          *reinterpret_cast<uint4*>(As + nxt * BM * LDK + a_lds[c]) = ra[c];
-#pragma unroll
-        for (int c = 0; c < C::B_CHUNKS; ++c)
-          *reinterpret_cast<uint4*>(Bs + nxt * BN * LDK + b_lds[c]) = rb[c];
-      }
-      __syncthreads();
-    }
-
-    // ---- epilogue: block (i, k) holds D[n][m], lane: m = l32, n = 8*(v/4) + 4*hi + v%4
+template <class C, int EPI>
+__device__ __forceinline__ void run_epilogue(const GemmArgs& a, floatx16 (&acc)[C::RN][C::RM], int m0,
+                                             int n0, int M, int wm, int wn, int l32, int hi) {
     if constexpr (EPI == EPI_QKV) {
       const int H = a.hidden;
       const int region = n0 / H;  // 0 q, 1 k, 2 v (BN divides H)
@@ -277,22 +168,208 @@ gemm_bf16_kernel(GemmArgs a) {
         }
       }
     } else {
+      // bias of this lane's output columns, hoisted out of the row loop
+      float bv[C::RN][4][4];
+#pragma unroll
+      for (int i = 0; i < C::RN; ++i)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int n = n0 + wn * C::WTN + i * 32 + 8 * g + 4 * hi;
+          if (a.bias) unpack4(*reinterpret_cast<const uint2*>(a.bias + n), bv[i][g]);
+          else bv[i][g][0] = bv[i][g][1] = bv[i][g][2] = bv[i][g][3] = 0.f;
+        }
+      const bool full = m0 + wm * C::WTM + C::WTM <= M;  // wave-uniform: no row past M
 #pragma unroll
       for (int k = 0; k < C::RM; ++k) {
         const int m = m0 + wm * C::WTM + k * 32 + l32;
-        if (m >= M) continue;
+        if (!full && m >= M) continue;
+        uint16_t* crow = a.C + (long)m * a.ldc;
+        const uint16_t* grow = nullptr;
+        if constexpr (EPI == EPI_GATE_RES) grow = a.gate + (long)a.row_req[m] * a.ld_gate;
 #pragma unroll
         for (int i = 0; i < C::RN; ++i) {
-          const int nb = n0 + wn * C::WTN + i * 32;
+          const int nb = n0 + wn * C::WTN + i * 32 + 4 * hi;
 #pragma unroll
           for (int g = 0; g < 4; ++g) {
-            float v4[4] = {acc[i][k][4 * g], acc[i][k][4 * g + 1], acc[i][k][4 * g + 2],
-                           acc[i][k][4 * g + 3]};
-            epilogue_store4<EPI>(a, m, nb + 8 * g + 4 * hi, v4);
+            const int n = nb + 8 * g;
+            float y[4];
+#pragma unroll
+            for (int t = 0; t < 4; ++t) y[t] = acc[i][k][4 * g + t] + bv[i][g][t];
+            if constexpr (EPI == EPI_F32) {
+              *reinterpret_cast<float4*>(a.Cf + (long)m * a.ldc + n) = make_float4(y[0], y[1], y[2], y[3]);
+              continue;
+            } else if constexpr (EPI == EPI_GELU) {
+#pragma unroll
+              for (int t = 0; t < 4; ++t) y[t] = gelu_tanh_f(rbf(y[t]));
+            } else if constexpr (EPI == EPI_GATE_RES) {
+              float gt[4], xr[4];
+              unpack4(*reinterpret_cast<const uint2*>(grow + n), gt);
+              unpack4(*reinterpret_cast<const uint2*>(crow + n), xr);
+#pragma unroll
+              for (int t = 0; t < 4; ++t) y[t] = xr[t] + rbf(gt[t] * rbf(y[t]));
+            }
+            // EPI_BIAS: one rounding, inside the pack
+            *reinterpret_cast<uint2*>(crow + n) = pack4(y[0], y[1], y[2], y[3]);
           }
         }
       }
     }
+}
+
+template <class C, int EPI>
+__global__ void __launch_bounds__(C::THREADS, C::WAVES_PER_EU)
+gemm_bf16_kernel(GemmArgs a) {
+  constexpr int BM = C::BM, BN = C::BN, BK = C::BK, ST = C::ST, CH = C::CH, TH = C::THREADS;
+  // one distinct LDS object per stage: the compiler can then prove that the DMA
+  // into one stage never aliases LDS reads of another, and inserts no wait for it
+  __shared__ __attribute__((aligned(1024))) uint16_t sA0[BM * BK], sB0[BN * BK];
+  __shared__ __attribute__((aligned(1024))) uint16_t sA1[ST > 1 ? BM * BK : 8], sB1[ST > 1 ? BN * BK : 8];
+  __shared__ __attribute__((aligned(1024))) uint16_t sA2[ST > 2 ? BM * BK : 8], sB2[ST > 2 ? BN * BK : 8];
+  __shared__ __attribute__((aligned(1024))) uint16_t sA3[ST > 3 ? BM * BK : 8], sB3[ST > 3 ? BN * BK : 8];
+  auto stA = [&](auto stc) -> uint16_t* {
+    constexpr int s = decltype(stc)::value;
+    if constexpr (s == 0) return sA0;
+    else if constexpr (s == 1) return sA1;
+    else if constexpr (s == 2) return sA2;
+    else return sA3;
+  };
+  auto stB = [&](auto stc) -> uint16_t* {
+    constexpr int s = decltype(stc)::value;
+    if constexpr (s == 0) return sB0;
+    else if constexpr (s == 1) return sB1;
+    else if constexpr (s == 2) return sB2;
+    else return sB3;
+  };
+
+  const int M = a.M_dev ? *a.M_dev : a.M;
+  const int N = a.N, K = a.K;
+  const int tiles_m = (M + BM - 1) / BM;
+  const int tiles_n = N / BN;
+  const int total = tiles_m * tiles_n;
+  if (total == 0) return;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wm = wave / C::WN, wn = wave % C::WN;
+  const int l32 = lane & 31, hi = lane >> 5;
+
+  // XCD-contiguous tile walk: workgroups with equal blockIdx.x % 8 share an XCD.
+  const int nxcd = 8;
+  const int xcd = blockIdx.x % nxcd;
+  const int slot = blockIdx.x / nxcd;
+  const int per_xcd = gridDim.x / nxcd;
+  const int chunk = (total + nxcd - 1) / nxcd;
+  auto tile_at = [&](int jt) { const int t = xcd * chunk + jt; return (jt < chunk && t < total) ? t : -1; };
+
+  // DMA: lane L of wave w, load j -> tile row j*RPR + w*ROWS_PER_DMA + L/CH, slot L%CH,
+  // i.e. source chunk (L%CH) ^ swz(row)
+  const int dma_row = wave * C::ROWS_PER_DMA + lane / CH;
+  int a_off[C::AJ], b_off[C::BJ];
+  auto set_offsets = [&](int tile) {
+    const int m0 = (tile / tiles_n) * BM, n0 = (tile % tiles_n) * BN;
+#pragma unroll
+    for (int j = 0; j < C::AJ; ++j) {
+      const int r = j * C::RPR + dma_row;
+      int gm = m0 + r;
+      gm = gm < M ? gm : M - 1;
+      a_off[j] = gm * (int)a.lda + (((lane % CH) ^ swz<CH>(r)) << 3);
+    }
+#pragma unroll
+    for (int j = 0; j < C::BJ; ++j) {
+      const int r = j * C::RPR + dma_row;
+      b_off[j] = (n0 + r) * (int)a.ldb + (((lane % CH) ^ swz<CH>(r)) << 3);
+    }
+  };
+  auto dma = [&](auto stc, int kstep) {
+    uint16_t* la = stA(stc);
+    uint16_t* lb = stB(stc);
+    const int koff = kstep * BK;
+#pragma unroll
+    for (int j = 0; j < C::AJ; ++j)
+      __builtin_amdgcn_global_load_lds(DFH_GPTR(a.A + a_off[j] + koff),
+                                       DFH_LPTR(la + (j * C::RPR + wave * C::ROWS_PER_DMA) * BK), 16, 0,
+                                       0);
+#pragma unroll
+    for (int j = 0; j < C::BJ; ++j)
+      __builtin_amdgcn_global_load_lds(DFH_GPTR(a.B + b_off[j] + koff),
+                                       DFH_LPTR(lb + (j * C::RPR + wave * C::ROWS_PER_DMA) * BK), 16, 0,
+                                       0);
+  };
+
+  const int fa_row = wm * C::WTM + l32;
+  const int fb_row = wn * C::WTN + l32;
+  floatx16 acc[C::RN][C::RM];
+  auto compute = [&](auto stc) {
+    const uint16_t* la = stA(stc);
+    const uint16_t* lb = stB(stc);
+#pragma unroll
+    for (int kk = 0; kk < BK / 16; ++kk) {
+      const int ch = 2 * kk + hi;
+      bf16x8 fa[C::RM], fb[C::RN];
+#pragma unroll
+      for (int i = 0; i < C::RM; ++i)
+        fa[i] = *reinterpret_cast<const bf16x8*>(la + lds_off<CH>(fa_row + i * 32, ch));
+#pragma unroll
+      for (int i = 0; i < C::RN; ++i)
+        fb[i] = *reinterpret_cast<const bf16x8*>(lb + lds_off<CH>(fb_row + i * 32, ch));
+#pragma unroll
+      for (int i = 0; i < C::RN; ++i)
+#pragma unroll
+        for (int k = 0; k < C::RM; ++k)
+          acc[i][k] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[i], fa[k], acc[i][k], 0, 0, 0);
+    }
+  };
+
+  const int KT = K / BK;
+  // one pipelined K step: k = step index, stage s = k % ST (compile-time)
+  auto step = [&](auto stc, int k) {
+    constexpr int s = decltype(stc)::value;
+    if (k >= KT) return;  // uniform
+    if (k == 0 || k + ST - 2 >= KT) wait_vm_lgkm0<0>();   // tile start / pipeline drain: exact
+    else wait_vm_lgkm0<(ST >= 2 ? (ST - 2) * C::LPS : 0)>();
+    __builtin_amdgcn_s_barrier();
+    if (k + ST - 1 < KT) dma(std::integral_constant<int, (s + ST - 1) % ST>{}, k + ST - 1);
+    compute(stc);
+  };
+  auto prologue = [&]() {
+    dma(std::integral_constant<int, 0>{}, 0);
+    if constexpr (ST > 2) { if (1 < KT) dma(std::integral_constant<int, 1 % ST>{}, 1); }
+    if constexpr (ST > 3) { if (2 < KT) dma(std::integral_constant<int, 2 % ST>{}, 2); }
+  };
+
+  int jt = slot;
+  int tile = tile_at(jt);
+  if (tile >= 0) {
+    set_offsets(tile);
+    prologue();
+  }
+  while (tile >= 0) {
+    const int m0 = (tile / tiles_n) * BM, n0 = (tile % tiles_n) * BN;
+#pragma unroll
+    for (int i = 0; i < C::RN; ++i)
+#pragma unroll
+      for (int k = 0; k < C::RM; ++k)
+#pragma unroll
+        for (int t = 0; t < 16; ++t) acc[i][k][t] = 0.f;
+    for (int k0 = 0; k0 < KT; k0 += ST) {
+      step(std::integral_constant<int, 0>{}, k0);
+      if constexpr (ST > 1) step(std::integral_constant<int, 1 % ST>{}, k0 + 1);
+      if constexpr (ST > 2) step(std::integral_constant<int, 2 % ST>{}, k0 + 2);
+      if constexpr (ST > 3) step(std::integral_constant<int, 3 % ST>{}, k0 + 3);
+    }
+    // every wave is done with every stage before it is refilled
+    wait_vm_lgkm0<0>();
+    __builtin_amdgcn_s_barrier();
+    // start the next tile's first K steps under this tile's epilogue
+    jt += per_xcd;
+    const int next = tile_at(jt);
+    if (next >= 0) {
+      set_offsets(next);
+      prologue();
+    }
+    run_epilogue<C, EPI>(a, acc, m0, n0, M, wm, wn, l32, hi);
+    tile = next;
   }
 }
 
@@ -309,60 +386,63 @@ int num_cus() {
   return g_num_cus;
 }
 
-template <int BM, int BN, int WM, int WN, int EPI>
+template <class C, int EPI>
 hipError_t launch(const GemmArgs& a, hipStream_t s) {
-  using C = Cfg<BM, BN, WM, WN>;
-  auto kern = gemm_bf16_kernel<BM, BN, WM, WN, EPI>;
-  static bool attr_set = false;
-  if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, C::LDS_BYTES);
-    if (e != hipSuccess) return e;
-    attr_set = true;
-  }
-  const long tiles_upper = (long)((a.M + BM - 1) / BM) * (a.N / BN);
-  const int wg_per_cu = (160 * 1024) / C::LDS_BYTES >= 2 ? 2 : 1;
-  long grid = (long)num_cus() * wg_per_cu;
+  auto kern = gemm_bf16_kernel<C, EPI>;
+  const long tiles_upper = (long)((a.M + C::BM - 1) / C::BM) * (a.N / C::BN);
+  long grid = (long)num_cus() * C::WG_PER_CU;
   if (tiles_upper < grid) grid = ((tiles_upper + 7) / 8) * 8;
   if (grid < 8) grid = 8;
-  dfh_launch(kern, dim3((unsigned)grid), dim3(C::THREADS), C::LDS_BYTES, s, a);
+  dfh_launch(kern, dim3((unsigned)grid), dim3(C::THREADS), 0, s, a);
   return hipGetLastError();
 }
+
+// tile configurations: (BM, BN, BK, stages, wave grid)
+using T0 = Cfg<256, 256, 64, 2, 2, 4>;  // 8 waves, 128x64 per wave, 128 KB LDS
+using T1 = Cfg<256, 256, 32, 4, 2, 4>;  // 8 waves, 4 stages of BK 32, 128 KB
+using T2 = Cfg<128, 128, 64, 2, 2, 2>;  // 4 waves, 64 KB: two workgroups per CU
+using T3 = Cfg<64, 64, 64, 2, 2, 2>;    // small problems
+using T4 = Cfg<256, 128, 64, 2, 2, 2>;  // 4 waves, 128x64 per wave, 96 KB
+using T5 = Cfg<128, 256, 32, 3, 2, 2>;  // 4 waves, 64x128 per wave, 72 KB: two per CU
+using T6 = Cfg<256, 128, 64, 3, 2, 2>;  // 4 waves, 3 stages, 144 KB
+using T7 = Cfg<128, 128, 32, 4, 2, 2>;  // 4 waves, 4 stages of BK 32, 64 KB: two per CU
+constexpr int kNumTiles = 8;
+const int kTileBM[kNumTiles] = {T0::BM, T1::BM, T2::BM, T3::BM, T4::BM, T5::BM, T6::BM, T7::BM};
+const int kTileBN[kNumTiles] = {T0::BN, T1::BN, T2::BN, T3::BN, T4::BN, T5::BN, T6::BN, T7::BN};
+const int kTileBK[kNumTiles] = {T0::BK, T1::BK, T2::BK, T3::BK, T4::BK, T5::BK, T6::BK, T7::BK};
+const int kTileWTN[kNumTiles] = {T0::WTN, T1::WTN, T2::WTN, T3::WTN, T4::WTN, T5::WTN, T6::WTN, T7::WTN};
 
 template <int EPI>
 hipError_t dispatch_tiles(const GemmArgs& a, hipStream_t s, int tile) {
   switch (tile) {
-    case 0: return launch<256, 256, 2, 2, EPI>(a, s);
-    case 1: return launch<256, 128, 2, 2, EPI>(a, s);
-    case 2: return launch<128, 128, 2, 2, EPI>(a, s);
-    case 3: return launch<64, 64, 2, 2, EPI>(a, s);
+    case 0: return launch<T0, EPI>(a, s);
+    case 1: return launch<T1, EPI>(a, s);
+    case 2: return launch<T2, EPI>(a, s);
+    case 3: return launch<T3, EPI>(a, s);
+    case 4: return launch<T4, EPI>(a, s);
+    case 5: return launch<T5, EPI>(a, s);
+    case 6: return launch<T6, EPI>(a, s);
+    case 7: return launch<T7, EPI>(a, s);
     default: return hipErrorInvalidValue;
   }
 }
 
-const int kTileBN[4] = {256, 128, 128, 64};
-const int kTileBM[4] = {256, 256, 128, 64};
-
 }  // namespace
 
 hipError_t gemm_bf16(const GemmArgs& a, int epi, hipStream_t s, int tile) {
-  if (a.K % BK != 0 || a.K <= 0 || a.N <= 0 || a.M < 0) return hipErrorInvalidValue;
+  if (a.K <= 0 || a.N <= 0 || a.M < 0 || a.K % 32 != 0) return hipErrorInvalidValue;
   if (a.M == 0) return hipSuccess;  // a.M is the host upper bound of rows
   if (tile < 0) {
-    // heuristic: big tiles for big problems, keep >= ~1 wave of tiles on the chip
+    const long cus = num_cus();
     const long t0 = (long)((a.M + 255) / 256) * (a.N / 256);
-    if (a.N % 256 == 0 && t0 >= 2L * num_cus()) tile = 0;
-    else if (a.N % 128 == 0 && (long)((a.M + 255) / 256) * (a.N / 128) >= num_cus()) tile = 1;
-    else if (a.N % 128 == 0 && (long)((a.M + 127) / 128) * (a.N / 128) >= num_cus() / 2) tile = 2;
+    if (a.N % 256 == 0 && a.K % 64 == 0 && t0 >= 2 * cus) tile = 0;
+    else if (a.N % 128 == 0 && a.K % 64 == 0 && (long)((a.M + 127) / 128) * (a.N / 128) >= cus) tile = 2;
     else tile = 3;
   }
-  if (tile < 0 || tile > 3) return hipErrorInvalidValue;
-  if (a.N % kTileBN[tile] != 0) return hipErrorInvalidValue;
-  if (epi == EPI_QKV) {
-    if (tile == 3) tile = 2;  // RoPE pairs need a 64-column wave tile
-    if (a.N % kTileBN[tile] != 0 || a.hidden % kTileBN[tile] != 0 || a.head_dim != 64)
-      return hipErrorInvalidValue;
-  }
+  if (tile < 0 || tile >= kNumTiles) return hipErrorInvalidValue;
+  if (epi == EPI_QKV && kTileWTN[tile] < 64) tile = 2;  // RoPE pairs need a 64-column wave tile
+  if (a.N % kTileBN[tile] != 0 || a.K % kTileBK[tile] != 0) return hipErrorInvalidValue;
+  if (epi == EPI_QKV && (a.hidden % kTileBN[tile] != 0 || a.head_dim != 64)) return hipErrorInvalidValue;
   // element offsets are 32-bit
   if ((long)a.M * a.lda >= (1L << 31) || (long)a.N * a.ldb >= (1L << 31)) return hipErrorInvalidValue;
   (void)kTileBM;

@@ -50,7 +50,10 @@ def _assert_latents(got, ref, ld, label):
 
 # ----------------------------------------------------------------------------- GEMM
 GEMM_CASES = [(1, 64, 64, 3), (37, 128, 256, 2), (300, 1024, 1024, -1), (700, 1024, 1024, 0),
-              (1000, 3072, 1024, 1), (513, 1024, 4096, -1), (64, 75776 // 8, 1024, -1)]
+              (1000, 3072, 1024, 1), (513, 1024, 4096, -1), (64, 75776 // 8, 1024, -1),
+              (777, 512, 1024, 4), (1500, 4096, 1024, 0), (20, 256, 64, 0), (333, 256, 192, 1),
+              (1111, 1024, 1024, 5), (600, 1024, 4096, 6), (259, 512, 1024, 7), (1234, 3072, 1024, 1),
+              (100, 512, 96, 7), (70, 256, 160, 5)]
 
 
 @pytest.mark.parametrize("M,N,K,tile", GEMM_CASES)
