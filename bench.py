@@ -28,6 +28,7 @@ sys.path.insert(0, ROOT)
 
 PEAK_BF16_TFLOPS = 2500.0      # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0
+PEAK_INT8_TOPS = 5000.0        # MI355X dense int8 MFMA
 FRAME_S = 0.04                 # one latent frame = 1920 samples at 48 kHz
 
 
@@ -69,6 +70,42 @@ def cpu_baseline(cfg, W, lens, hist, noise, budget_s: float):
     }
 
 
+def w8a8_bench(reps: int = 20):
+    """W8A8 linears in isolation at the largest token count of that configuration
+    (M = 16384): activation quantisation + i8 MFMA GEMM with fused dequant/bias."""
+    import torch
+    from nanovllm_dots_amd.int8 import gemm_w8a8, quant_act, quant_weight
+    M = 16384
+    out = {}
+    for K, N in [(1024, 3072), (1024, 1024), (1024, 4096), (4096, 1024)]:
+        g = torch.Generator(device="cpu").manual_seed(K + N)
+        x = torch.randn(M, K, generator=g).bfloat16().cuda()
+        w = (0.02 * torch.randn(N, K, generator=g)).bfloat16().cuda()
+        b = torch.zeros(N, device="cuda", dtype=torch.bfloat16)
+        wq, sw = quant_weight(w)
+        xq, sx = quant_act(x)
+        gemm_w8a8(xq, wq, sx, sw, b)
+        torch.cuda.synchronize()
+        e = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+        e[0].record()
+        for _ in range(reps):
+            xq, sx = quant_act(x)
+        e[1].record()
+        for _ in range(reps):
+            gemm_w8a8(xq, wq, sx, sw, b)
+        e[2].record()
+        torch.cuda.synchronize()
+        q_ms = e[0].elapsed_time(e[1]) / reps
+        g_ms = e[1].elapsed_time(e[2]) / reps
+        ops = 2 * M * K * N
+        out[f"K{K}_N{N}"] = {"gemm_tops": round(ops / g_ms / 1e9, 1),
+                             "gemm_frac_int8_peak": round(ops / g_ms / 1e9 / PEAK_INT8_TOPS, 4),
+                             "quant_GBps": round(M * K * 3 / q_ms / 1e6, 1),
+                             "linear_tops": round(ops / (g_ms + q_ms) / 1e9, 1)}
+        log(f"w8a8 K={K} N={N}: gemm {out[f'K{K}_N{N}']['gemm_tops']} TOPS, quant {q_ms*1e3:.1f} us")
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -78,6 +115,7 @@ def main():
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--cpu-budget", type=float, default=20.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-w8a8", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the FM head shards requests across GPUs with no "
@@ -150,6 +188,8 @@ def main():
     gemm_ms = sum(classes[k][0] for k in per_launch) / args.steps
     log("per-class ms/solve: " + ", ".join(f"{k}={v['ms_per_solve']:.3f}" for k, v in breakdown.items()))
 
+    w8 = None if args.no_w8a8 else w8a8_bench()
+
     cpu = None
     if not args.no_cpu:
         cpu = cpu_baseline(cfg, W, lens, hist, noise, args.cpu_budget)
@@ -173,6 +213,7 @@ def main():
                      "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": None,
                      "avg_launch_ms": round(avg_ms, 5), "flops_per_launch": per_launch[dom]},
         "kernel_breakdown": breakdown,
+        "w8a8_m16384": w8,
         "cpu_baseline": ({k: (round(v, 5) if isinstance(v, float) else v) for k, v in cpu.items()
                           if k in ("value", "unit", "cores", "kind", "sample")} if cpu else None),
         "cpu_xRT": round(cpu["xRT"], 4) if cpu else None,

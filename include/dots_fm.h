@@ -127,6 +127,20 @@ int dfh_profile_read(DfhHandle* h, double* ms_per_class, long* launches_per_clas
 int dfh_gemm_bf16(const void* A, long lda, const void* B, long ldb, void* C, long ldc,
                   const void* bias, int M, int N, int K, int epilogue, int tile, void* stream);
 
+/* W8A8 linear (Int8DynamicLinear, int8_dit.py:34-65).
+ * Per-row dynamic activation quantisation of bf16 x [M, K] in bf16 arithmetic
+ * (int8_dit.py:57-58): q int8 [M, K], scale f32 [M] (bf16 values). */
+int dfh_quant_act_i8(const void* x, long ldx, void* q, long ldq, void* scale, int M, int K, void* stream);
+/* Per-output-channel weight quantisation in float32 (int8_dit.py:40-45) of bf16
+ * W [N, K]: q int8 [N, K] (row-major, K contiguous: the transpose of the
+ * reference's Wt_int8 [K, N]), scale f32 [N]. */
+int dfh_quant_weight_i8(const void* w, void* q, void* scale, int N, int K, void* stream);
+/* acc[m, n] = sum_k xq[m, k] * wq[n, k] in int32 (== torch._int_mm(xq, wq^T)).
+ * out_int32 = 1: out int32 [M, N]; else out bf16 = ((acc * sx[m]) * sw[n]) + bias[n]
+ * (bias bf16 or NULL). K a multiple of 64; ldx/ldw in bytes, ldo in elements. */
+int dfh_gemm_w8a8(const void* xq, long ldx, const void* wq, long ldw, void* out, long ldo, const void* sx,
+                  const void* sw, const void* bias, int M, int N, int K, int out_int32, int tile, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

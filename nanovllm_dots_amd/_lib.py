@@ -66,6 +66,10 @@ SIGNATURES = {
     "dfh_profile_read": (C.c_int, [vp, C.POINTER(C.c_double), C.POINTER(C.c_long), C.c_int]),
     "dfh_gemm_bf16": (C.c_int, [vp, C.c_long, vp, C.c_long, vp, C.c_long, vp, C.c_int, C.c_int,
                                 C.c_int, C.c_int, C.c_int, vp]),
+    "dfh_quant_act_i8": (C.c_int, [vp, C.c_long, vp, C.c_long, vp, C.c_int, C.c_int, vp]),
+    "dfh_quant_weight_i8": (C.c_int, [vp, vp, vp, C.c_int, C.c_int, vp]),
+    "dfh_gemm_w8a8": (C.c_int, [vp, C.c_long, vp, C.c_long, vp, C.c_long, vp, vp, vp, C.c_int, C.c_int,
+                                C.c_int, C.c_int, C.c_int, vp]),
 }
 
 _lib = None

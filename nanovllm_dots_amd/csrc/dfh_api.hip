@@ -612,4 +612,43 @@ int dfh_gemm_bf16(const void* A, long lda, const void* B, long ldb, void* C, lon
   return 0;
 }
 
+int dfh_quant_act_i8(const void* x, long ldx, void* q, long ldq, void* scale, int M, int K, void* stream) {
+  if (!x || !q || !scale) return fail("dfh_quant_act_i8: NULL pointer");
+  if (M < 0 || K <= 0 || K % 8 || ldx % 8 || ldq % 8 || ldx < K || ldq < K)
+    return fail("dfh_quant_act_i8: K, ldx, ldq must be multiples of 8 with ld >= K (M=%d K=%d)", M, K);
+  hipError_t e = quant_rows_bf16(reinterpret_cast<const uint16_t*>(x), ldx, reinterpret_cast<int8_t*>(q), ldq,
+                                 reinterpret_cast<float*>(scale), M, K, reinterpret_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail("dfh_quant_act_i8: %s", hipGetErrorString(e));
+  return 0;
+}
+
+int dfh_quant_weight_i8(const void* w, void* q, void* scale, int N, int K, void* stream) {
+  if (!w || !q || !scale) return fail("dfh_quant_weight_i8: NULL pointer");
+  if (N < 0 || K <= 0) return fail("dfh_quant_weight_i8: bad shape N=%d K=%d", N, K);
+  hipError_t e = quant_weight_f32(reinterpret_cast<const uint16_t*>(w), reinterpret_cast<int8_t*>(q),
+                                  reinterpret_cast<float*>(scale), N, K, reinterpret_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail("dfh_quant_weight_i8: %s", hipGetErrorString(e));
+  return 0;
+}
+
+int dfh_gemm_w8a8(const void* xq, long ldx, const void* wq, long ldw, void* out, long ldo, const void* sx,
+                  const void* sw, const void* bias, int M, int N, int K, int out_int32, int tile, void* stream) {
+  if (!xq || !wq || !out) return fail("dfh_gemm_w8a8: NULL pointer");
+  if (!out_int32 && (!sx || !sw)) return fail("dfh_gemm_w8a8: dequantised output needs both scales");
+  if (K % 64 || ldx % 16 || ldw % 16 || ldx < K || ldw < K || ldo < N || ldo % 4)
+    return fail("dfh_gemm_w8a8: K must be a multiple of 64, ldx/ldw multiples of 16 (M=%d N=%d K=%d)", M, N, K);
+  GemmArgs a;
+  memset(&a, 0, sizeof(a));
+  a.A = reinterpret_cast<const uint16_t*>(xq); a.lda = ldx;
+  a.B = reinterpret_cast<const uint16_t*>(wq); a.ldb = ldw;
+  a.C = reinterpret_cast<uint16_t*>(out); a.Ci = reinterpret_cast<int*>(out); a.ldc = ldo;
+  a.sx = reinterpret_cast<const float*>(sx); a.sw = reinterpret_cast<const float*>(sw);
+  a.bias = reinterpret_cast<const uint16_t*>(bias);
+  a.M = M; a.N = N; a.K = K;
+  hipError_t e = gemm_i8(a, out_int32 ? EPI_I32 : EPI_DQ, reinterpret_cast<hipStream_t>(stream), tile);
+  if (e != hipSuccess)
+    return fail("dfh_gemm_w8a8(M=%d N=%d K=%d tile=%d): %s", M, N, K, tile, hipGetErrorString(e));
+  return 0;
+}
+
 }  // extern "C"

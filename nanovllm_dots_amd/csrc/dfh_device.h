@@ -13,6 +13,17 @@ typedef int intx16 __attribute__((ext_vector_type(16)));
 
 #define DFH_WAVE 64
 
+// float32 multiply / add that the compiler may not fuse into an FMA: sequences
+// that reproduce torch's separately rounded elementwise ops use these.
+__device__ __forceinline__ float mul_rn(float a, float b) {
+#pragma clang fp contract(off)
+  return a * b;
+}
+__device__ __forceinline__ float add_rn(float a, float b) {
+#pragma clang fp contract(off)
+  return a + b;
+}
+
 __device__ __forceinline__ float bf2f(bf16_t h) { return __uint_as_float(((uint32_t)h) << 16); }
 
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));

@@ -22,6 +22,8 @@ enum Epilogue : int {
   EPI_GATE_RES = 2,  // C = bf16(C + bf16(gate[req(m)] * bf16(acc + bias)))   (in place)
   EPI_QKV = 3,       // q|k -> C (optional qk-norm, RoPE), v -> V^T (transposed)
   EPI_F32 = 4,       // Cf = acc + bias (float32 out; tests)
+  EPI_I32 = 5,       // int8 operands: Ci = int32 accumulators
+  EPI_DQ = 6,        // int8 operands: C = bf16(((float(acc) * sx[m]) * sw[n]) + bias[n])
 };
 
 struct GemmArgs {
@@ -29,6 +31,8 @@ struct GemmArgs {
   const uint16_t* B; long ldb;       // [N, K] bf16 weights (nn.Linear layout)
   uint16_t* C; long ldc;             // [M, N] bf16 output
   float* Cf;                         // float32 output (EPI_F32)
+  int* Ci;                           // int32 output (EPI_I32)
+  const float* sx; const float* sw;  // EPI_DQ: per-row and per-column scales
   const uint16_t* bias;              // [N] or null
   int M; const int* M_dev;           // rows; M_dev (device int) overrides M when non-null
   int N, K;
@@ -47,6 +51,17 @@ struct GemmArgs {
 // Picks a tile shape for (M, N, K) and launches the persistent MFMA kernel.
 // Returns hipSuccess or an error (shape not supported / launch failure).
 hipError_t gemm_bf16(const GemmArgs& a, int epi, hipStream_t s, int tile_hint = -1);
+
+// int8 x int8 -> int32 GEMM (A [M, K] int8, B [N, K] int8, K-contiguous) with the
+// EPI_I32 or EPI_DQ epilogue. lda/ldb/K are given in BYTES (int8 elements).
+hipError_t gemm_i8(const GemmArgs& a, int epi, hipStream_t s, int tile_hint = -1);
+
+// Per-row dynamic int8 quantisation of a bf16 [M, K] matrix (Int8DynamicLinear,
+// int8_dit.py:57-58): s = max(bf16(amax/127), bf16(1e-8)); q = clamp(rint(bf16(x/s)), +-127).
+hipError_t quant_rows_bf16(const uint16_t* x, long ldx, int8_t* q, long ldq, float* scale, int M, int K,
+                           hipStream_t s);
+// Per-output-channel int8 weight quantisation in float32 (int8_dit.py:40-45).
+hipError_t quant_weight_f32(const uint16_t* w, int8_t* q, float* scale, int N, int K, hipStream_t s);
 
 // Row kernels -------------------------------------------------------------------
 // LayerNorm (no affine, fp32 stats) + adaLN modulate:

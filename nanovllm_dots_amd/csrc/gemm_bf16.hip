@@ -67,6 +67,23 @@ __device__ __forceinline__ int lds_off(int row, int chunk) {
   return row * (CH * 8) + ((chunk ^ swz<CH>(row)) << 3);
 }
 
+// MFMA flavours sharing the tile machinery. An int8 row of K bytes has the byte
+// layout of a bf16 row of K/2 elements, so the DMA / LDS / fragment code works
+// on 16-bit units for both; one 16-byte fragment is 8 bf16 or 16 int8 values.
+struct OpBf16 {
+  using acc_t = floatx16;
+  __device__ static __forceinline__ acc_t mma(const bf16x8& a, const bf16x8& b, const acc_t& c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  }
+};
+struct OpI8 {
+  using acc_t = intx16;
+  __device__ static __forceinline__ acc_t mma(const bf16x8& a, const bf16x8& b, const acc_t& c) {
+    return __builtin_amdgcn_mfma_i32_32x32x32_i8(__builtin_bit_cast(intx4, a), __builtin_bit_cast(intx4, b),
+                                                  c, 0, 0, 0);
+  }
+};
+
 // s_waitcnt vmcnt(n) lgkmcnt(0) (gfx9 encoding: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt_hi[15:14])
 template <int N>
 __device__ __forceinline__ void wait_vm_lgkm0() {
@@ -76,8 +93,8 @@ __device__ __forceinline__ void wait_vm_lgkm0() {
 
 
 
-template <class C, int EPI>
-__device__ __forceinline__ void run_epilogue(const GemmArgs& a, floatx16 (&acc)[C::RN][C::RM], int m0,
+template <class C, int EPI, class ACC>
+__device__ __forceinline__ void run_epilogue(const GemmArgs& a, ACC (&acc)[C::RN][C::RM], int m0,
                                              int n0, int M, int wm, int wn, int l32, int hi) {
     if constexpr (EPI == EPI_QKV) {
       const int H = a.hidden;
@@ -148,8 +165,8 @@ __device__ __forceinline__ void run_epilogue(const GemmArgs& a, floatx16 (&acc)[
             for (int v = 0; v < 16; ++v) {
               const int d = 8 * (v >> 2) + 4 * hi + (v & 3);
               const float c = cs[d], s = sn[d];
-              const float r0 = __fadd_rn(__fmul_rn(x0[v], c), __fmul_rn(-x1[v], s));
-              const float r1 = __fadd_rn(__fmul_rn(x1[v], c), __fmul_rn(x0[v], s));
+              const float r0 = add_rn(mul_rn(x0[v], c), mul_rn(-x1[v], s));
+              const float r1 = add_rn(mul_rn(x1[v], c), mul_rn(x0[v], s));
               x0[v] = r0;
               x1[v] = r1;
             }
@@ -168,8 +185,9 @@ __device__ __forceinline__ void run_epilogue(const GemmArgs& a, floatx16 (&acc)[
         }
       }
     } else {
-      // bias of this lane's output columns, hoisted out of the row loop
+      // bias (and int8 weight scale) of this lane's output columns, hoisted out of the row loop
       float bv[C::RN][4][4];
+      float swv[C::RN][4][4];
 #pragma unroll
       for (int i = 0; i < C::RN; ++i)
 #pragma unroll
@@ -177,6 +195,10 @@ __device__ __forceinline__ void run_epilogue(const GemmArgs& a, floatx16 (&acc)[
           const int n = n0 + wn * C::WTN + i * 32 + 8 * g + 4 * hi;
           if (a.bias) unpack4(*reinterpret_cast<const uint2*>(a.bias + n), bv[i][g]);
           else bv[i][g][0] = bv[i][g][1] = bv[i][g][2] = bv[i][g][3] = 0.f;
+          if constexpr (EPI == EPI_DQ) {
+            const float4 w4 = *reinterpret_cast<const float4*>(a.sw + n);
+            swv[i][g][0] = w4.x; swv[i][g][1] = w4.y; swv[i][g][2] = w4.z; swv[i][g][3] = w4.w;
+          }
         }
       const bool full = m0 + wm * C::WTM + C::WTM <= M;  // wave-uniform: no row past M
 #pragma unroll
@@ -186,6 +208,8 @@ __device__ __forceinline__ void run_epilogue(const GemmArgs& a, floatx16 (&acc)[
         uint16_t* crow = a.C + (long)m * a.ldc;
         const uint16_t* grow = nullptr;
         if constexpr (EPI == EPI_GATE_RES) grow = a.gate + (long)a.row_req[m] * a.ld_gate;
+        float sxm = 0.f;
+        if constexpr (EPI == EPI_DQ) sxm = a.sx[m];
 #pragma unroll
         for (int i = 0; i < C::RN; ++i) {
           const int nb = n0 + wn * C::WTN + i * 32 + 4 * hi;
@@ -193,8 +217,19 @@ __device__ __forceinline__ void run_epilogue(const GemmArgs& a, floatx16 (&acc)[
           for (int g = 0; g < 4; ++g) {
             const int n = nb + 8 * g;
             float y[4];
+            if constexpr (EPI == EPI_I32) {
+              *reinterpret_cast<int4*>(a.Ci + (long)m * a.ldc + n) =
+                  make_int4(acc[i][k][4 * g], acc[i][k][4 * g + 1], acc[i][k][4 * g + 2], acc[i][k][4 * g + 3]);
+              continue;
+            } else if constexpr (EPI == EPI_DQ) {
+              // ((acc.f32 * s_x) * s_w) + bias, each op rounded to float32 (int8_dit.py:60-62)
 #pragma unroll
-            for (int t = 0; t < 4; ++t) y[t] = acc[i][k][4 * g + t] + bv[i][g][t];
+              for (int t = 0; t < 4; ++t)
+                y[t] = add_rn(mul_rn(mul_rn((float)acc[i][k][4 * g + t], sxm), swv[i][g][t]), bv[i][g][t]);
+            } else {
+#pragma unroll
+              for (int t = 0; t < 4; ++t) y[t] = acc[i][k][4 * g + t] + bv[i][g][t];
+            }
             if constexpr (EPI == EPI_F32) {
               *reinterpret_cast<float4*>(a.Cf + (long)m * a.ldc + n) = make_float4(y[0], y[1], y[2], y[3]);
               continue;
@@ -216,9 +251,9 @@ __device__ __forceinline__ void run_epilogue(const GemmArgs& a, floatx16 (&acc)[
     }
 }
 
-template <class C, int EPI>
+template <class C, class Op, int EPI>
 __global__ void __launch_bounds__(C::THREADS, C::WAVES_PER_EU)
-gemm_bf16_kernel(GemmArgs a) {
+gemm_mfma_kernel(GemmArgs a) {
   constexpr int BM = C::BM, BN = C::BN, BK = C::BK, ST = C::ST, CH = C::CH, TH = C::THREADS;
   // one distinct LDS object per stage: the compiler can then prove that the DMA
   // into one stage never aliases LDS reads of another, and inserts no wait for it
@@ -299,7 +334,7 @@ gemm_bf16_kernel(GemmArgs a) {
 
   const int fa_row = wm * C::WTM + l32;
   const int fb_row = wn * C::WTN + l32;
-  floatx16 acc[C::RN][C::RM];
+  typename Op::acc_t acc[C::RN][C::RM];
   auto compute = [&](auto stc) {
     const uint16_t* la = stA(stc);
     const uint16_t* lb = stB(stc);
@@ -317,7 +352,7 @@ gemm_bf16_kernel(GemmArgs a) {
       for (int i = 0; i < C::RN; ++i)
 #pragma unroll
         for (int k = 0; k < C::RM; ++k)
-          acc[i][k] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[i], fa[k], acc[i][k], 0, 0, 0);
+          acc[i][k] = Op::mma(fb[i], fa[k], acc[i][k]);
     }
   };
 
@@ -351,7 +386,7 @@ gemm_bf16_kernel(GemmArgs a) {
 #pragma unroll
       for (int k = 0; k < C::RM; ++k)
 #pragma unroll
-        for (int t = 0; t < 16; ++t) acc[i][k][t] = 0.f;
+        for (int t = 0; t < 16; ++t) acc[i][k][t] = 0;
     for (int k0 = 0; k0 < KT; k0 += ST) {
       step(std::integral_constant<int, 0>{}, k0);
       if constexpr (ST > 1) step(std::integral_constant<int, 1 % ST>{}, k0 + 1);
@@ -386,9 +421,9 @@ int num_cus() {
   return g_num_cus;
 }
 
-template <class C, int EPI>
+template <class C, class Op, int EPI>
 hipError_t launch(const GemmArgs& a, hipStream_t s) {
-  auto kern = gemm_bf16_kernel<C, EPI>;
+  auto kern = gemm_mfma_kernel<C, Op, EPI>;
   const long tiles_upper = (long)((a.M + C::BM - 1) / C::BM) * (a.N / C::BN);
   long grid = (long)num_cus() * C::WG_PER_CU;
   if (tiles_upper < grid) grid = ((tiles_upper + 7) / 8) * 8;
@@ -412,19 +447,27 @@ const int kTileBN[kNumTiles] = {T0::BN, T1::BN, T2::BN, T3::BN, T4::BN, T5::BN, 
 const int kTileBK[kNumTiles] = {T0::BK, T1::BK, T2::BK, T3::BK, T4::BK, T5::BK, T6::BK, T7::BK};
 const int kTileWTN[kNumTiles] = {T0::WTN, T1::WTN, T2::WTN, T3::WTN, T4::WTN, T5::WTN, T6::WTN, T7::WTN};
 
-template <int EPI>
+template <class Op, int EPI>
 hipError_t dispatch_tiles(const GemmArgs& a, hipStream_t s, int tile) {
   switch (tile) {
-    case 0: return launch<T0, EPI>(a, s);
-    case 1: return launch<T1, EPI>(a, s);
-    case 2: return launch<T2, EPI>(a, s);
-    case 3: return launch<T3, EPI>(a, s);
-    case 4: return launch<T4, EPI>(a, s);
-    case 5: return launch<T5, EPI>(a, s);
-    case 6: return launch<T6, EPI>(a, s);
-    case 7: return launch<T7, EPI>(a, s);
+    case 0: return launch<T0, Op, EPI>(a, s);
+    case 1: return launch<T1, Op, EPI>(a, s);
+    case 2: return launch<T2, Op, EPI>(a, s);
+    case 3: return launch<T3, Op, EPI>(a, s);
+    case 4: return launch<T4, Op, EPI>(a, s);
+    case 5: return launch<T5, Op, EPI>(a, s);
+    case 6: return launch<T6, Op, EPI>(a, s);
+    case 7: return launch<T7, Op, EPI>(a, s);
     default: return hipErrorInvalidValue;
   }
+}
+
+int pick_tile(const GemmArgs& a) {
+  const long cus = num_cus();
+  const long t0 = (long)((a.M + 255) / 256) * (a.N / 256);
+  if (a.N % 256 == 0 && a.K % 64 == 0 && t0 >= 2 * cus) return 0;
+  if (a.N % 128 == 0 && a.K % 64 == 0 && (long)((a.M + 127) / 128) * (a.N / 128) >= cus) return 2;
+  return 3;
 }
 
 }  // namespace
@@ -432,13 +475,7 @@ hipError_t dispatch_tiles(const GemmArgs& a, hipStream_t s, int tile) {
 hipError_t gemm_bf16(const GemmArgs& a, int epi, hipStream_t s, int tile) {
   if (a.K <= 0 || a.N <= 0 || a.M < 0 || a.K % 32 != 0) return hipErrorInvalidValue;
   if (a.M == 0) return hipSuccess;  // a.M is the host upper bound of rows
-  if (tile < 0) {
-    const long cus = num_cus();
-    const long t0 = (long)((a.M + 255) / 256) * (a.N / 256);
-    if (a.N % 256 == 0 && a.K % 64 == 0 && t0 >= 2 * cus) tile = 0;
-    else if (a.N % 128 == 0 && a.K % 64 == 0 && (long)((a.M + 127) / 128) * (a.N / 128) >= cus) tile = 2;
-    else tile = 3;
-  }
+  if (tile < 0) tile = pick_tile(a);
   if (tile < 0 || tile >= kNumTiles) return hipErrorInvalidValue;
   if (epi == EPI_QKV && kTileWTN[tile] < 64) tile = 2;  // RoPE pairs need a 64-column wave tile
   if (a.N % kTileBN[tile] != 0 || a.K % kTileBK[tile] != 0) return hipErrorInvalidValue;
@@ -447,11 +484,32 @@ hipError_t gemm_bf16(const GemmArgs& a, int epi, hipStream_t s, int tile) {
   if ((long)a.M * a.lda >= (1L << 31) || (long)a.N * a.ldb >= (1L << 31)) return hipErrorInvalidValue;
   (void)kTileBM;
   switch (epi) {
-    case EPI_BIAS: return dispatch_tiles<EPI_BIAS>(a, s, tile);
-    case EPI_GELU: return dispatch_tiles<EPI_GELU>(a, s, tile);
-    case EPI_GATE_RES: return dispatch_tiles<EPI_GATE_RES>(a, s, tile);
-    case EPI_QKV: return dispatch_tiles<EPI_QKV>(a, s, tile);
-    case EPI_F32: return dispatch_tiles<EPI_F32>(a, s, tile);
+    case EPI_BIAS: return dispatch_tiles<OpBf16, EPI_BIAS>(a, s, tile);
+    case EPI_GELU: return dispatch_tiles<OpBf16, EPI_GELU>(a, s, tile);
+    case EPI_GATE_RES: return dispatch_tiles<OpBf16, EPI_GATE_RES>(a, s, tile);
+    case EPI_QKV: return dispatch_tiles<OpBf16, EPI_QKV>(a, s, tile);
+    case EPI_F32: return dispatch_tiles<OpBf16, EPI_F32>(a, s, tile);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+hipError_t gemm_i8(const GemmArgs& a_bytes, int epi, hipStream_t s, int tile) {
+  // byte-sized K and leading dimensions -> 16-bit units of the shared tile machinery
+  if (a_bytes.K <= 0 || a_bytes.K % 64 != 0 || a_bytes.lda % 16 != 0 || a_bytes.ldb % 16 != 0)
+    return hipErrorInvalidValue;
+  if (a_bytes.N <= 0 || a_bytes.M < 0) return hipErrorInvalidValue;
+  if (a_bytes.M == 0) return hipSuccess;
+  GemmArgs a = a_bytes;
+  a.K = a_bytes.K / 2;
+  a.lda = a_bytes.lda / 2;
+  a.ldb = a_bytes.ldb / 2;
+  if (tile < 0) tile = pick_tile(a);
+  if (tile < 0 || tile >= kNumTiles) return hipErrorInvalidValue;
+  if (a.N % kTileBN[tile] != 0 || a.K % kTileBK[tile] != 0) return hipErrorInvalidValue;
+  if ((long)a.M * a.lda >= (1L << 31) || (long)a.N * a.ldb >= (1L << 31)) return hipErrorInvalidValue;
+  switch (epi) {
+    case EPI_I32: return dispatch_tiles<OpI8, EPI_I32>(a, s, tile);
+    case EPI_DQ: return dispatch_tiles<OpI8, EPI_DQ>(a, s, tile);
     default: return hipErrorInvalidValue;
   }
 }

@@ -54,9 +54,9 @@ ln_modulate_kernel(const uint16_t* __restrict__ x, long ldx, uint16_t* __restric
     unpack4(*reinterpret_cast<const uint2*>(scp + col), sc);
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
-      const float ln = __fmul_rn(v[4 * j + t] - mean, rstd);
+      const float ln = mul_rn(v[4 * j + t] - mean, rstd);
       const float onep = rbf(1.0f + sc[t]);
-      y[t] = __fadd_rn(__fmul_rn(ln, onep), sh[t]);
+      y[t] = add_rn(mul_rn(ln, onep), sh[t]);
     }
     *reinterpret_cast<uint2*>(op + col) = pack4(y[0], y[1], y[2], y[3]);
   }
@@ -160,7 +160,7 @@ __global__ void rope_table_kernel(const float* __restrict__ inv_freq, int half, 
   const int idx = blockIdx.x * blockDim.x + threadIdx.x;
   if (idx >= max_pos * half) return;
   const int p = idx / half, d = idx % half;
-  const float f = __fmul_rn((float)p, inv_freq[d]);
+  const float f = mul_rn((float)p, inv_freq[d]);
   cosv[idx] = cosf(f);
   sinv[idx] = sinf(f);
 }
@@ -176,8 +176,8 @@ __global__ void temb_kernel(const float* __restrict__ tv, TimeVals tvh, int rows
   const float t = tv ? tv[r] : tvh.v[r];
   for (int k = threadIdx.x; k < dim; k += blockDim.x) {
     float e = 0.f;
-    if (k < half) e = cosf(__fmul_rn(t, freqs[k]));
-    else if (k < 2 * half) e = sinf(__fmul_rn(t, freqs[k - half]));
+    if (k < half) e = cosf(mul_rn(t, freqs[k]));
+    else if (k < 2 * half) e = sinf(mul_rn(t, freqs[k - half]));
     out[(long)r * dim + k] = f2bf(e);
   }
 }
