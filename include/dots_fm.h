@@ -19,6 +19,9 @@
  *                          nanovllm_dots/models/dots/native/layers.py:82-84, 152-161
  *   dfh_quant_act_i8, dfh_quant_weight_i8, dfh_gemm_w8a8
  *                       <- Int8DynamicLinear nanovllm_dots/models/dots/int8_dit.py:34-65
+ *   dfh_kvcache_*       <- FMCache / extend_cache / active_forward
+ *                          nanovllm_dots/models/dots/cached_fm.py:82-197 (CFG flow matching
+ *                          there; restated for the MeanFlow DiT)
  */
 #ifndef DOTS_FM_H
 #define DOTS_FM_H
@@ -28,6 +31,7 @@ extern "C" {
 #endif
 
 typedef struct DfhHandle DfhHandle;
+typedef struct DfhKVCache DfhKVCache;
 
 /* DiT shape. Mirrors the checkpoint config's DiT block
  * (nanovllm_dots/models/dots/native/config.py:46-47, loader.py:52-67) and the core
@@ -140,6 +144,26 @@ int dfh_quant_weight_i8(const void* w, void* q, void* scale, int N, int K, void*
  * (bias bf16 or NULL). K a multiple of 64; ldx/ldw in bytes, ldo in elements. */
 int dfh_gemm_w8a8(const void* xq, long ldx, const void* wq, long ldw, void* out, long ldo, const void* sx,
                   const void* sw, const void* bias, int M, int N, int K, int out_int32, int tile, void* stream);
+
+/* Prefix K/V cache of a MeanFlow solve (per-(timestep, layer) cache of
+ * cached_fm.py:82-197, FMCache / extend_cache / active_forward, restated for the
+ * MeanFlow DiT: c_k = T(t_k) + D(dt_k) + g, one branch). Each of n_streams
+ * streams holds up to `capacity` rows (prefix + the 1 + P active rows).
+ * dfh_kvcache_extend appends counts[i] history rows of stream i (FM sequence
+ * space, before input_layer; rows bf16 [n, m_max, H]) at every timestep: they
+ * attend causally to the cached prefix and each other (extend_cache).
+ * dfh_kvcache_solve runs the NFE-step MeanFlow solve of the active rows — the
+ * last hidden row (bf16 [n, H], position = prefix length) and P latent rows —
+ * against the cache (active_forward); it equals the full-recompute solve of
+ * the sequence prefix + last hidden row. t/dt grids: host [num_steps]. */
+int dfh_kvcache_create(DfhHandle* h, int n_streams, int capacity, int num_steps, DfhKVCache** out);
+int dfh_kvcache_destroy(DfhKVCache* c);
+int dfh_kvcache_reset(DfhKVCache* c, void* stream);
+int dfh_kvcache_lengths(DfhKVCache* c, int* lens);
+int dfh_kvcache_extend(DfhKVCache* c, const void* rows, int m_max, const int* counts, const void* g_cond,
+                       const float* t_grid, const float* dt_grid, void* stream);
+int dfh_kvcache_solve(DfhKVCache* c, const void* last_hidden, const void* g_cond, const void* noise, void* out,
+                      const float* t_grid, const float* dt_grid, void* stream);
 
 #ifdef __cplusplus
 }

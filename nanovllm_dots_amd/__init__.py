@@ -3,8 +3,8 @@
 Hand-written gfx950 HIP kernels (libdotsfm.so, C ABI in include/dots_fm.h)
 behind the reference's accelerator entry points (``fm_accel="hip"``).
 """
-from .hip_meanflow import (FMSpec, HipDiT, HipFMHead, HipMeanflow, batched_meanflow,  # noqa: F401
+from .hip_meanflow import (FMSpec, HipDiT, HipFMCache, HipFMHead, HipMeanflow, batched_meanflow,  # noqa: F401
                            meanflow_grid, rope_inv_freq, timestep_freqs)
 
-__all__ = ["FMSpec", "HipDiT", "HipFMHead", "HipMeanflow", "batched_meanflow", "meanflow_grid",
+__all__ = ["FMSpec", "HipDiT", "HipFMCache", "HipFMHead", "HipMeanflow", "batched_meanflow", "meanflow_grid",
            "rope_inv_freq", "timestep_freqs"]

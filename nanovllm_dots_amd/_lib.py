@@ -70,6 +70,13 @@ SIGNATURES = {
     "dfh_quant_weight_i8": (C.c_int, [vp, vp, vp, C.c_int, C.c_int, vp]),
     "dfh_gemm_w8a8": (C.c_int, [vp, C.c_long, vp, C.c_long, vp, C.c_long, vp, vp, vp, C.c_int, C.c_int,
                                 C.c_int, C.c_int, C.c_int, vp]),
+    "dfh_kvcache_create": (C.c_int, [vp, C.c_int, C.c_int, C.c_int, C.POINTER(vp)]),
+    "dfh_kvcache_destroy": (C.c_int, [vp]),
+    "dfh_kvcache_reset": (C.c_int, [vp, vp]),
+    "dfh_kvcache_lengths": (C.c_int, [vp, C.POINTER(C.c_int)]),
+    "dfh_kvcache_extend": (C.c_int, [vp, vp, C.c_int, C.POINTER(C.c_int), vp, C.POINTER(C.c_float),
+                                     C.POINTER(C.c_float), vp]),
+    "dfh_kvcache_solve": (C.c_int, [vp, vp, vp, vp, vp, C.POINTER(C.c_float), C.POINTER(C.c_float), vp]),
 }
 
 _lib = None

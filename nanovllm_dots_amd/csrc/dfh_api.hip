@@ -92,7 +92,7 @@ struct DfhHandle {
   int cap_n = 0, cap_T = 0, cap_S = 0;
   long cap_M = 0, ld_vt = 0;
   DevBuf seq, x, hbuf, qk, attn, ff, vt;
-  DevBuf row_req, row_pos, vt_col, cu_rows, cu_vt, hist_len, counts, err, patch_rows;
+  DevBuf row_req, row_pos, vt_col, cu_rows, cu_vt, hist_len, counts, err, patch_rows, seqs;
   DevBuf rope_cos, rope_sin;
   DevBuf temb_in, t_hid, t_out, d_hid, d_out, cond, cond_act, mod;
   DevBuf z, zp, fin, vel, tvals;
@@ -160,32 +160,46 @@ GemmArgs linear_args(const uint16_t* A, long lda, const uint16_t* W, const uint1
   return a;
 }
 
-int reserve(DfhHandle* h, int n, int T, int S, hipStream_t s) {
+// row-sized workspace (packed rows of one pass)
+int reserve_rows(DfhHandle* h, long M, hipStream_t s) {
+  if (M <= h->cap_M) return 0;
   const DfhConfig& c = h->cfg;
-  if (n <= h->cap_n && T <= h->cap_T && S <= h->cap_S && (long)n * T <= h->cap_M) return 0;
   DFH_CHECK(hipStreamSynchronize(s));  // in-flight kernels may still use the old buffers
-  const int nn = n > h->cap_n ? n : h->cap_n;
-  const int TT = T > h->cap_T ? T : h->cap_T;
-  const int SS = S > h->cap_S ? S : h->cap_S;
-  const long M = (long)nn * TT;
-  const long H = c.hidden, F = c.ffn, P = c.patch, ld = c.latent_dim;
-  const long ld_vt = M + 8L * nn + 128;
+  const long H = c.hidden, F = c.ffn, ld = c.latent_dim;
   DFH_CHECK(dev_alloc(h->seq, M * H * 2));
   DFH_CHECK(dev_alloc(h->x, M * H * 2));
   DFH_CHECK(dev_alloc(h->hbuf, M * H * 2));
   DFH_CHECK(dev_alloc(h->qk, M * 2 * H * 2));
   DFH_CHECK(dev_alloc(h->attn, M * H * 2));
   DFH_CHECK(dev_alloc(h->ff, M * F * 2));
-  DFH_CHECK(dev_alloc(h->vt, (size_t)H * ld_vt * 2));
   DFH_CHECK(dev_alloc(h->row_req, M * 4));
   DFH_CHECK(dev_alloc(h->row_pos, M * 4));
   DFH_CHECK(dev_alloc(h->vt_col, M * 4));
+  DFH_CHECK(dev_alloc(h->fin, M * H * 2));
+  DFH_CHECK(dev_alloc(h->vel, M * ld * 2));
+  h->cap_M = M;
+  return 0;
+}
+
+int reserve(DfhHandle* h, int n, int T, int S, hipStream_t s) {
+  const DfhConfig& c = h->cfg;
+  if (reserve_rows(h, (long)n * T, s)) return 1;
+  if (n <= h->cap_n && T <= h->cap_T && S <= h->cap_S && h->ld_vt >= (long)n * T + 8L * n + 128) return 0;
+  DFH_CHECK(hipStreamSynchronize(s));
+  const int nn = n > h->cap_n ? n : h->cap_n;
+  const int TT = T > h->cap_T ? T : h->cap_T;
+  const int SS = S > h->cap_S ? S : h->cap_S;
+  const long M = (long)nn * TT;
+  const long H = c.hidden, P = c.patch, ld = c.latent_dim;
+  const long ld_vt = M + 8L * nn + 128;
+  DFH_CHECK(dev_alloc(h->vt, (size_t)H * ld_vt * 2));
   DFH_CHECK(dev_alloc(h->cu_rows, (nn + 1) * 4));
   DFH_CHECK(dev_alloc(h->cu_vt, (nn + 1) * 4));
   DFH_CHECK(dev_alloc(h->hist_len, nn * 4));
   DFH_CHECK(dev_alloc(h->counts, 16));
   DFH_CHECK(dev_alloc(h->err, 16));
   DFH_CHECK(dev_alloc(h->patch_rows, nn * P * 4));
+  DFH_CHECK(dev_alloc(h->seqs, (long)nn * SS * sizeof(AttnSeq)));
   DFH_CHECK(dev_alloc(h->rope_cos, (size_t)TT * 32 * 4));
   DFH_CHECK(dev_alloc(h->rope_sin, (size_t)TT * 32 * 4));
   const long RS = (long)SS > nn ? SS : nn;  // timestep rows: per step (solve) or per request (forward)
@@ -199,13 +213,10 @@ int reserve(DfhHandle* h, int n, int T, int S, hipStream_t s) {
   DFH_CHECK(dev_alloc(h->mod, (long)SS * nn * h->ld_mod * 2));
   DFH_CHECK(dev_alloc(h->z, nn * P * ld * 2));
   DFH_CHECK(dev_alloc(h->zp, nn * P * H * 2));
-  DFH_CHECK(dev_alloc(h->fin, M * H * 2));
-  DFH_CHECK(dev_alloc(h->vel, M * ld * 2));
   DFH_CHECK(dev_alloc(h->tvals, (size_t)(2 * RS + 64) * 4));
   h->cap_n = nn;
   h->cap_T = TT;
   h->cap_S = SS;
-  h->cap_M = M;
   h->ld_vt = ld_vt;
   return 0;
 }
@@ -246,17 +257,37 @@ int build_modulation(DfhHandle* h, int S, int N, bool per_request_t, const float
   return 0;
 }
 
-// One DiT forward over the packed rows held in h->seq (M rows, device count in
-// counts[0]); modulation rows for this pass start at mod_row0 (request i uses
-// row mod_row0 + i). Writes the block output to h->x.
-int dit_blocks(DfhHandle* h, int n, int T, long mod_row0, hipStream_t s) {
+// One pass of the DiT blocks over packed rows. Input rows are in h->seq
+// (before input_layer); the block output lands in h->x. Row m uses modulation
+// row mod_row0 + row_req[m], RoPE position row_pos[m], writes its q|k row to
+// qk[l] row c_rows[m] (or m) and its V^T column vt_col[m] in vt[l].
+struct Pass {
+  int Mup = 0;                 // host upper bound of rows (grid sizes)
+  const int* Md = nullptr;     // device row count (null: Mup rows exactly)
+  long mod_row0 = 0;
+  const int* row_req = nullptr;
+  const int* row_pos = nullptr;
+  const int* c_rows = nullptr;
+  const int* vt_col = nullptr;
+  std::vector<uint16_t*> qk;   // per layer
+  long ldqk = 0;
+  std::vector<uint16_t*> vt;   // per layer
+  long ld_vt = 0;
+  const AttnSeq* seqs = nullptr;
+  int n_seq = 0, max_q = 0, max_kv = 0;
+  bool decode = false;         // split-KV decode attention (<= 32 queries / sequence)
+  float* part = nullptr;       // decode partials
+  bool kv_only_last = false;   // prefix pass: the last block only has to leave its K/V
+};
+
+int run_blocks(DfhHandle* h, const Pass& p, hipStream_t s) {
   const DfhConfig& c = h->cfg;
   const int H = c.hidden, F = c.ffn;
-  const int Mup = n * T;
-  const int* Md = P<int>(h->counts);
-  const uint16_t* mod = P<uint16_t>(h->mod) + mod_row0 * h->ld_mod;
+  const int Mup = p.Mup;
+  const int* Md = p.Md;
+  const uint16_t* mod = P<uint16_t>(h->mod) + p.mod_row0 * h->ld_mod;
   const long ldm = h->ld_mod;
-  int* row_req = P<int>(h->row_req);
+  const int* row_req = p.row_req;
 
   // input_layer
   DFH_CHECK(gemm(h, PC_OTHER, linear_args(P<uint16_t>(h->seq), H, h->in_w, h->in_b,
@@ -267,20 +298,24 @@ int dit_blocks(DfhHandle* h, int n, int T, long mod_row0, hipStream_t s) {
     prof_arm(h, PC_LN);
     DFH_CHECK(ln_modulate(P<uint16_t>(h->x), H, P<uint16_t>(h->hbuf), H, ml + 0 * H, ml + 1 * H, ldm,
                           row_req, nullptr, Mup, Md, H, c.ln_eps, s));
-    GemmArgs q = linear_args(P<uint16_t>(h->hbuf), H, h->qkv_w[l], h->qkv_b[l], P<uint16_t>(h->qk),
-                             2 * H, Mup, Md, 3 * H, H);
+    GemmArgs q = linear_args(P<uint16_t>(h->hbuf), H, h->qkv_w[l], h->qkv_b[l], p.qk[l], p.ldqk, Mup, Md,
+                             3 * H, H);
     q.hidden = H; q.head_dim = c.head_dim;
     q.rope_cos = c.rotary ? P<float>(h->rope_cos) : nullptr;
     q.rope_sin = c.rotary ? P<float>(h->rope_sin) : nullptr;
-    q.row_pos = P<int>(h->row_pos);
+    q.row_pos = p.row_pos;
     q.qk_norm = c.qk_norm;
     q.qn_w = h->qn_w[l]; q.qn_b = h->qn_b[l]; q.kn_w = h->kn_w[l]; q.kn_b = h->kn_b[l];
-    q.vt = P<uint16_t>(h->vt); q.ld_vt = h->ld_vt; q.vt_col = P<int>(h->vt_col);
+    q.vt = p.vt[l]; q.ld_vt = p.ld_vt; q.vt_col = p.vt_col; q.c_rows = p.c_rows;
     DFH_CHECK(gemm(h, PC_QKV, q, EPI_QKV, s, tile_for(Mup, 3 * H, H, kRoleQKV)));
+    if (p.kv_only_last && l == c.n_blocks - 1) break;
     prof_arm(h, PC_ATTN);
-    DFH_CHECK(fm_attention(P<uint16_t>(h->qk), 2 * H, P<uint16_t>(h->vt), h->ld_vt,
-                           P<uint16_t>(h->attn), H, P<int>(h->cu_rows), P<int>(h->cu_vt),
-                           P<int>(h->hist_len), n, c.patch, c.heads, T, s));
+    if (p.decode)
+      DFH_CHECK(decode_attention(p.qk[l], p.ldqk, p.vt[l], p.ld_vt, P<uint16_t>(h->attn), H, p.seqs, p.n_seq,
+                                 c.heads, p.max_kv, p.part, s));
+    else
+      DFH_CHECK(seq_attention(p.qk[l], p.ldqk, p.vt[l], p.ld_vt, P<uint16_t>(h->attn), H, p.seqs, p.n_seq,
+                              c.heads, p.max_q, s));
     GemmArgs o = linear_args(P<uint16_t>(h->attn), H, h->o_w[l], h->o_b[l], P<uint16_t>(h->x), H,
                              Mup, Md, H, H);
     o.gate = ml + 2 * H; o.ld_gate = ldm; o.row_req = row_req;
@@ -299,10 +334,32 @@ int dit_blocks(DfhHandle* h, int n, int T, long mod_row0, hipStream_t s) {
   return 0;
 }
 
+// The FM pass over the packed requests of layout(): rows m of h->seq, request
+// row_req[m], q|k into the workspace, V^T in h->vt.
+int dit_blocks(DfhHandle* h, int n, int T, long mod_row0, hipStream_t s) {
+  const DfhConfig& c = h->cfg;
+  Pass p;
+  p.Mup = n * T;
+  p.Md = P<int>(h->counts);
+  p.mod_row0 = mod_row0;
+  p.row_req = P<int>(h->row_req);
+  p.row_pos = P<int>(h->row_pos);
+  p.vt_col = P<int>(h->vt_col);
+  p.qk.assign(c.n_blocks, P<uint16_t>(h->qk));
+  p.ldqk = 2 * c.hidden;
+  p.vt.assign(c.n_blocks, P<uint16_t>(h->vt));
+  p.ld_vt = h->ld_vt;
+  p.seqs = P<AttnSeq>(h->seqs);
+  p.n_seq = n;
+  p.max_q = T;
+  return run_blocks(h, p, s);
+}
+
 int layout(DfhHandle* h, int n, int T, const void* pos_ids, const void* inp, hipStream_t s) {
   const DfhConfig& c = h->cfg;
   DFH_CHECK(fm_layout(reinterpret_cast<const float*>(pos_ids), n, T, c.patch, P<int>(h->cu_rows),
-                      P<int>(h->cu_vt), P<int>(h->hist_len), P<int>(h->counts), P<int>(h->err), s));
+                      P<int>(h->cu_vt), P<int>(h->hist_len), P<int>(h->counts), P<int>(h->err),
+                      P<AttnSeq>(h->seqs), s));
   DFH_CHECK(fm_gather(reinterpret_cast<const uint16_t*>(inp), n, T, c.patch, c.hidden,
                       P<int>(h->cu_rows), P<int>(h->cu_vt), P<int>(h->hist_len), P<uint16_t>(h->seq),
                       P<int>(h->row_req), P<int>(h->row_pos), P<int>(h->vt_col),
@@ -346,7 +403,7 @@ int dfh_destroy(DfhHandle* h) {
   (void)hipDeviceSynchronize();
   DevBuf* bufs[] = {&h->w_arena, &h->consts, &h->seq, &h->x, &h->hbuf, &h->qk, &h->attn, &h->ff,
                     &h->vt, &h->row_req, &h->row_pos, &h->vt_col, &h->cu_rows, &h->cu_vt,
-                    &h->hist_len, &h->counts, &h->err, &h->patch_rows, &h->rope_cos, &h->rope_sin,
+                    &h->hist_len, &h->counts, &h->err, &h->patch_rows, &h->seqs, &h->rope_cos, &h->rope_sin,
                     &h->temb_in, &h->t_hid, &h->t_out, &h->d_hid, &h->d_out, &h->cond,
                     &h->cond_act, &h->mod, &h->z, &h->zp, &h->fin, &h->vel, &h->tvals};
   for (DevBuf* b : bufs)
@@ -649,6 +706,265 @@ int dfh_gemm_w8a8(const void* xq, long ldx, const void* wq, long ldw, void* out,
   if (e != hipSuccess)
     return fail("dfh_gemm_w8a8(M=%d N=%d K=%d tile=%d): %s", M, N, K, tile, hipGetErrorString(e));
   return 0;
+}
+
+}  // extern "C"
+
+// ===========================================================================
+// Prefix K/V cache of a MeanFlow solve (the per-(timestep, layer) cache of
+// nanovllm_dots/models/dots/cached_fm.py:82-197 for the MeanFlow DiT).
+// History rows attend causally among themselves, so at a fixed timestep their
+// K/V never depend on the latent: they are computed once per timestep (all
+// timesteps in one batched prefix pass) and kept; each solver step then runs
+// only the 1 + P active rows, which see the cached prefix and each other.
+// Slab layout per layer: q|k rows [S*n*cap, 2H] and V^T [H, S*n*cap + 256];
+// region (k, i) = rows / columns [(k*n + i) * cap, +cap) holds stream i's prefix
+// at timestep k, followed by scratch slots for the step's active rows.
+struct DfhKVCache {
+  DfhHandle* h = nullptr;
+  int n = 0, S = 0, cap = 0;
+  long rows_total = 0, ld_vt = 0;
+  std::vector<DevBuf> qk, vt;
+  DevBuf lens, counts, offs, seqs, c_rows, row_req, row_pos, vt_col, patch_rows, lh_rows, part, z;
+  long table_rows = 0;
+  std::vector<int> lens_host;
+  int* pinned = nullptr;  // 2n+1 ints staged for uploads
+};
+
+namespace {
+
+int cache_tables(DfhKVCache* c, long rows, hipStream_t s) {
+  if (rows <= c->table_rows) return 0;
+  DFH_CHECK(hipStreamSynchronize(s));
+  DFH_CHECK(dev_alloc(c->c_rows, rows * 4));
+  DFH_CHECK(dev_alloc(c->row_req, rows * 4));
+  DFH_CHECK(dev_alloc(c->row_pos, rows * 4));
+  DFH_CHECK(dev_alloc(c->vt_col, rows * 4));
+  c->table_rows = rows;
+  return 0;
+}
+
+Pass cache_pass(DfhKVCache* c) {
+  DfhHandle* h = c->h;
+  Pass p;
+  for (int l = 0; l < h->cfg.n_blocks; ++l) {
+    p.qk.push_back(P<uint16_t>(c->qk[l]));
+    p.vt.push_back(P<uint16_t>(c->vt[l]));
+  }
+  p.ldqk = 2 * h->cfg.hidden;
+  p.ld_vt = c->ld_vt;
+  return p;
+}
+
+// Append counts[i] rows (FM sequence space, before input_layer) to each
+// stream's prefix at every timestep. rows: device bf16, stream i's rows start at
+// rows + i * stride (elements), consecutive rows H apart. counts/offs: device.
+int cache_extend_dev(DfhKVCache* c, const uint16_t* rows, long stride, int m_max, int Mtot, int max_count,
+                     const uint16_t* g, const TimeVals& tv, const TimeVals& dtv, hipStream_t s) {
+  DfhHandle* h = c->h;
+  const DfhConfig& cf = h->cfg;
+  const long total = (long)c->S * Mtot;
+  if (total == 0) return 0;
+  if (total * 4L * cf.ffn >= (1L << 31)) return fail("kv cache extend: %ld rows too many for one pass", total);
+  if (reserve(h, c->n, c->cap, c->S, s)) return 1;  // RoPE positions up to cap
+  if (reserve_rows(h, total, s)) return 1;
+  if (cache_tables(c, total, s)) return 1;
+  // positions up to cap
+  DFH_CHECK(rope_table(P<float>(h->consts), cf.head_dim / 2, c->cap, P<float>(c->h->rope_cos),
+                       P<float>(c->h->rope_sin), s));
+  if (build_modulation(h, c->S, c->n, false, nullptr, nullptr, tv, dtv, true, g, s)) return 1;
+  DFH_CHECK(prefix_tables(rows, stride, m_max, cf.hidden, P<int>(c->counts), P<int>(c->lens), P<int>(c->offs),
+                          c->n, c->S, c->cap, P<uint16_t>(h->seq), P<int>(c->row_req), P<int>(c->row_pos),
+                          P<int>(c->c_rows), P<int>(c->vt_col), P<AttnSeq>(c->seqs), s));
+  Pass p = cache_pass(c);
+  p.Mup = (int)total;
+  p.row_req = P<int>(c->row_req);
+  p.row_pos = P<int>(c->row_pos);
+  p.c_rows = P<int>(c->c_rows);
+  p.vt_col = P<int>(c->vt_col);
+  p.seqs = P<AttnSeq>(c->seqs);
+  p.n_seq = c->S * c->n;
+  p.max_q = max_count;
+  p.kv_only_last = true;
+  if (run_blocks(h, p, s)) return 1;
+  DFH_CHECK(cache_advance(P<int>(c->lens), P<int>(c->counts), c->n, s));
+  return 0;
+}
+
+// NFE-step solve of the active rows against the cache.
+int cache_solve(DfhKVCache* c, const uint16_t* last_hidden, const int* lh_src_rows, const uint16_t* g,
+                const uint16_t* noise, uint16_t* out, const TimeVals& tv, const TimeVals& dtv, int max_len,
+                hipStream_t s) {
+  DfhHandle* h = c->h;
+  const DfhConfig& cf = h->cfg;
+  const int n = c->n, S = c->S, Pp = cf.patch, R = 1 + Pp, H = cf.hidden, ld = cf.latent_dim;
+  const int rows = n * R;
+  if (reserve(h, n, c->cap, S, s)) return 1;
+  if (reserve_rows(h, rows, s)) return 1;
+  if (cache_tables(c, (long)S * rows, s)) return 1;
+  DFH_CHECK(rope_table(P<float>(h->consts), cf.head_dim / 2, c->cap, P<float>(h->rope_cos),
+                       P<float>(h->rope_sin), s));
+  if (build_modulation(h, S, n, false, nullptr, nullptr, tv, dtv, true, g, s)) return 1;
+  DFH_CHECK(active_tables(P<int>(c->lens), n, S, Pp, c->cap, P<int>(c->row_req), P<int>(c->row_pos),
+                          P<int>(c->c_rows), P<int>(c->vt_col), P<AttnSeq>(c->seqs), P<int>(c->patch_rows),
+                          P<int>(c->lh_rows), s));
+  // the last hidden rows of the active block (they stay put across steps)
+  DFH_CHECK(gather_rows(last_hidden, lh_src_rows, P<int>(c->lh_rows), n, H, P<uint16_t>(h->seq), s));
+  DFH_CHECK(hipMemcpyAsync(c->z.p, noise, (size_t)n * Pp * ld * 2, hipMemcpyDeviceToDevice, s));
+  const int NP = n * Pp;
+  for (int st = 0; st < S; ++st) {
+    DFH_CHECK(gemm(h, PC_OTHER, linear_args(P<uint16_t>(c->z), ld, h->coord_w, h->coord_b,
+                                            P<uint16_t>(h->zp), H, NP, nullptr, H, ld), EPI_BIAS, s));
+    DFH_CHECK(scatter_rows(P<uint16_t>(h->zp), P<int>(c->patch_rows), NP, H, P<uint16_t>(h->seq), s));
+    Pass p = cache_pass(c);
+    p.Mup = rows;
+    p.row_req = P<int>(c->row_req) + (long)st * rows;
+    p.row_pos = P<int>(c->row_pos) + (long)st * rows;
+    p.c_rows = P<int>(c->c_rows) + (long)st * rows;
+    p.vt_col = P<int>(c->vt_col) + (long)st * rows;
+    p.seqs = P<AttnSeq>(c->seqs) + (long)st * n;
+    p.n_seq = n;
+    p.max_kv = max_len + R;
+    p.decode = true;
+    p.part = P<float>(c->part);
+    if (run_blocks(h, p, s)) return 1;
+    const uint16_t* mf = P<uint16_t>(h->mod) + (long)cf.n_blocks * 6 * H;
+    prof_arm(h, PC_LN);
+    DFH_CHECK(ln_modulate(P<uint16_t>(h->x), H, P<uint16_t>(h->fin), H, mf, mf + H, h->ld_mod,
+                          p.row_req, P<int>(c->patch_rows), NP, nullptr, H, cf.ln_eps, s));
+    DFH_CHECK(gemm(h, PC_OTHER, linear_args(P<uint16_t>(h->fin), H, h->fin_w, h->fin_b,
+                                            P<uint16_t>(h->vel), ld, NP, nullptr, ld, H), EPI_BIAS, s));
+    DFH_CHECK(z_update(P<uint16_t>(c->z), P<uint16_t>(h->vel), dtv.v[st], (long)NP * ld, s));
+  }
+  DFH_CHECK(hipMemcpyAsync(out, c->z.p, (size_t)NP * ld * 2, hipMemcpyDeviceToDevice, s));
+  return 0;
+}
+
+int cache_alloc(DfhHandle* h, int n, int cap, int S, DfhKVCache** out) {
+  const DfhConfig& cf = h->cfg;
+  DfhKVCache* c = new DfhKVCache();
+  c->h = h; c->n = n; c->S = S; c->cap = cap;
+  c->rows_total = (long)S * n * cap;
+  c->ld_vt = c->rows_total + 256;
+  c->qk.resize(cf.n_blocks);
+  c->vt.resize(cf.n_blocks);
+  auto bail = [&](hipError_t e) {
+    for (auto& b : c->qk) if (b.p) (void)hipFree(b.p);
+    for (auto& b : c->vt) if (b.p) (void)hipFree(b.p);
+    delete c;
+    return fail("kv cache allocation: %s", hipGetErrorString(e));
+  };
+  for (int l = 0; l < cf.n_blocks; ++l) {
+    hipError_t e = dev_alloc(c->qk[l], (size_t)c->rows_total * 2 * cf.hidden * 2);
+    if (e == hipSuccess) e = dev_alloc(c->vt[l], (size_t)cf.hidden * c->ld_vt * 2);
+    if (e != hipSuccess) return bail(e);
+  }
+  DevBuf* small[] = {&c->lens, &c->counts, &c->offs};
+  for (DevBuf* b : small) {
+    hipError_t e = dev_alloc(*b, (size_t)(n + 1) * 4);
+    if (e != hipSuccess) return bail(e);
+  }
+  const int n_chunks = (cap + 255) / 256;
+  hipError_t e = dev_alloc(c->seqs, (size_t)S * n * sizeof(AttnSeq));
+  if (e == hipSuccess) e = dev_alloc(c->patch_rows, (size_t)n * cf.patch * 4);
+  if (e == hipSuccess) e = dev_alloc(c->lh_rows, (size_t)n * 4);
+  if (e == hipSuccess) e = dev_alloc(c->part, (size_t)n * cf.heads * n_chunks * 32 * 66 * 4);
+  if (e == hipSuccess) e = dev_alloc(c->z, (size_t)n * cf.patch * cf.latent_dim * 2);
+  if (e == hipSuccess) e = hipHostMalloc(reinterpret_cast<void**>(&c->pinned), (2 * n + 2) * sizeof(int));
+  if (e != hipSuccess) return bail(e);
+  c->lens_host.assign(n, 0);
+  *out = c;
+  return 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+int dfh_kvcache_create(DfhHandle* h, int n_streams, int capacity, int num_steps, DfhKVCache** out) {
+  if (!h || !out) return fail("null argument");
+  if (!h->weights_set) return fail("dfh_kvcache_create: weights not set");
+  if (n_streams <= 0 || n_streams > 1024 || num_steps <= 0 || num_steps > kMaxTimeVals)
+    return fail("dfh_kvcache_create: bad n_streams=%d num_steps=%d", n_streams, num_steps);
+  if (capacity < h->cfg.patch + 2) return fail("dfh_kvcache_create: capacity %d too small", capacity);
+  const int cap = (capacity + 7) & ~7;  // region starts stay 16-byte aligned in V^T
+  if ((long)num_steps * n_streams * cap * 2 * h->cfg.hidden >= (1L << 31))
+    return fail("dfh_kvcache_create: cache too large for 32-bit offsets");
+  return cache_alloc(h, n_streams, cap, num_steps, out);
+}
+
+int dfh_kvcache_destroy(DfhKVCache* c) {
+  if (!c) return 0;
+  (void)hipDeviceSynchronize();
+  for (auto& b : c->qk) if (b.p) (void)hipFree(b.p);
+  for (auto& b : c->vt) if (b.p) (void)hipFree(b.p);
+  DevBuf* bufs[] = {&c->lens, &c->counts, &c->offs, &c->seqs, &c->c_rows, &c->row_req, &c->row_pos,
+                    &c->vt_col, &c->patch_rows, &c->lh_rows, &c->part, &c->z};
+  for (DevBuf* b : bufs) if (b->p) (void)hipFree(b->p);
+  if (c->pinned) (void)hipHostFree(c->pinned);
+  delete c;
+  return 0;
+}
+
+int dfh_kvcache_reset(DfhKVCache* c, void* stream) {
+  if (!c) return fail("null cache");
+  DFH_CHECK(hipMemsetAsync(c->lens.p, 0, (size_t)c->n * 4, reinterpret_cast<hipStream_t>(stream)));
+  c->lens_host.assign(c->n, 0);
+  return 0;
+}
+
+int dfh_kvcache_lengths(DfhKVCache* c, int* lens) {
+  if (!c || !lens) return fail("null argument");
+  for (int i = 0; i < c->n; ++i) lens[i] = c->lens_host[i];
+  return 0;
+}
+
+int dfh_kvcache_extend(DfhKVCache* c, const void* rows, int m_max, const int* counts, const void* g_cond,
+                       const float* t_grid, const float* dt_grid, void* stream) {
+  if (!c || !rows || !counts || !t_grid || !dt_grid) return fail("dfh_kvcache_extend: NULL argument");
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const int R = 1 + c->h->cfg.patch;
+  int Mtot = 0, max_count = 0;
+  for (int i = 0; i < c->n; ++i) {
+    if (counts[i] < 0 || counts[i] > m_max) return fail("dfh_kvcache_extend: counts[%d]=%d", i, counts[i]);
+    if (c->lens_host[i] + counts[i] + R > c->cap)
+      return fail("dfh_kvcache_extend: stream %d would hold %d rows (+%d active) > capacity %d", i,
+                  c->lens_host[i] + counts[i], R, c->cap);
+    Mtot += counts[i];
+    max_count = counts[i] > max_count ? counts[i] : max_count;
+  }
+  if (Mtot == 0) return 0;
+  // stage counts and their exclusive prefix sums (the pinned buffer is free once the stream is idle)
+  DFH_CHECK(hipStreamSynchronize(s));
+  int acc = 0;
+  for (int i = 0; i < c->n; ++i) { c->pinned[i] = counts[i]; c->pinned[c->n + 1 + i] = acc; acc += counts[i]; }
+  c->pinned[2 * c->n + 1] = acc;
+  DFH_CHECK(hipMemcpyAsync(c->counts.p, c->pinned, (size_t)c->n * 4, hipMemcpyHostToDevice, s));
+  DFH_CHECK(hipMemcpyAsync(c->offs.p, c->pinned + c->n + 1, (size_t)(c->n + 1) * 4, hipMemcpyHostToDevice, s));
+  TimeVals tv{}, dtv{};
+  for (int k = 0; k < c->S; ++k) { tv.v[k] = t_grid[k]; dtv.v[k] = dt_grid[k]; }
+  const int H = c->h->cfg.hidden;
+  if (cache_extend_dev(c, reinterpret_cast<const uint16_t*>(rows), (long)m_max * H, m_max, Mtot, max_count,
+                       reinterpret_cast<const uint16_t*>(g_cond), tv, dtv, s))
+    return 1;
+  for (int i = 0; i < c->n; ++i) c->lens_host[i] += counts[i];
+  return 0;
+}
+
+int dfh_kvcache_solve(DfhKVCache* c, const void* last_hidden, const void* g_cond, const void* noise, void* out,
+                      const float* t_grid, const float* dt_grid, void* stream) {
+  if (!c || !last_hidden || !noise || !out || !t_grid || !dt_grid) return fail("dfh_kvcache_solve: NULL argument");
+  const int R = 1 + c->h->cfg.patch;
+  int max_len = 0;
+  for (int i = 0; i < c->n; ++i) {
+    if (c->lens_host[i] + R > c->cap) return fail("dfh_kvcache_solve: stream %d prefix too long", i);
+    max_len = c->lens_host[i] > max_len ? c->lens_host[i] : max_len;
+  }
+  TimeVals tv{}, dtv{};
+  for (int k = 0; k < c->S; ++k) { tv.v[k] = t_grid[k]; dtv.v[k] = dt_grid[k]; }
+  return cache_solve(c, reinterpret_cast<const uint16_t*>(last_hidden), nullptr,
+                     reinterpret_cast<const uint16_t*>(g_cond), reinterpret_cast<const uint16_t*>(noise),
+                     reinterpret_cast<uint16_t*>(out), tv, dtv, max_len, reinterpret_cast<hipStream_t>(stream));
 }
 
 }  // extern "C"

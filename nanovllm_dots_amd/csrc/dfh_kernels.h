@@ -46,6 +46,7 @@ struct GemmArgs {
   const uint16_t* qn_w; const uint16_t* qn_b;    // [head_dim]
   const uint16_t* kn_w; const uint16_t* kn_b;
   uint16_t* vt; long ld_vt; const int* vt_col;   // V^T [hidden, ld_vt]; column of row m = vt_col[m]
+  const int* c_rows;                             // optional: q|k output row of row m
 };
 
 // Picks a tile shape for (M, N, K) and launches the persistent MFMA kernel.
@@ -71,11 +72,30 @@ hipError_t ln_modulate(const uint16_t* x, long ldx, uint16_t* out, long ldo,
                        const int* row_req, const int* row_map, int rows_upper, const int* M_dev,
                        int H, float eps, hipStream_t s);
 
-// Varlen FM-mask attention (head_dim 64). qk: [M, 2H] (q | k), vt: [H, ld_vt].
-hipError_t fm_attention(const uint16_t* qk, long ldqk, const uint16_t* vt, long ld_vt,
-                        uint16_t* out, long ldo, const int* cu_rows, const int* cu_vt,
-                        const int* hist_len, int n_req, int patch, int heads, int max_T,
-                        hipStream_t s);
+// One attention sequence (device array element). Rows index the q|k buffer
+// ([rows, 2H]: q in columns [0, H), k in [H, 2H)); V^T is [H, ld_vt].
+struct AttnSeq {
+  int q_row0;      // q|k row of query position 0
+  int kv_row0;     // q|k row of key position 0
+  int vt_col0;     // V^T column of key position 0 (multiple of 8)
+  int q_begin, q_end;  // query positions computed
+  int causal_end;  // queries below it see keys [0, q]; the others [0, kv_len)
+  int kv_len;
+  int out_row0;    // output row of query position 0
+};
+
+// Varlen attention with the implicit FM mask (head_dim 64), one workgroup per
+// 128 queries of one (sequence, head). max_q bounds q_end - q_begin.
+hipError_t seq_attention(const uint16_t* qk, long ldqk, const uint16_t* vt, long ld_vt, uint16_t* out,
+                         long ldo, const AttnSeq* seqs, int n_seq, int heads, int max_q, hipStream_t s);
+
+// Split-KV decode attention: every query of a sequence sees all kv_len keys
+// (q_begin..q_end are at most 32 queries). Keys are read straight from HBM in
+// chunks of kv_chunk keys per workgroup; partials go to `part` and are merged.
+// part holds n_seq * heads * ceil(max_kv / kv_chunk) * 32 * 66 floats.
+hipError_t decode_attention(const uint16_t* qk, long ldqk, const uint16_t* vt, long ld_vt, uint16_t* out,
+                            long ldo, const AttnSeq* seqs, int n_seq, int heads, int max_kv,
+                            float* part, hipStream_t s);
 
 }  // namespace dfh
 

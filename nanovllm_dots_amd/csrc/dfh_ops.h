@@ -3,6 +3,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "dfh_kernels.h"
+
 namespace dfh {
 
 constexpr int kMaxTimeVals = 16;
@@ -11,7 +13,14 @@ struct TimeVals {
 };
 
 hipError_t fm_layout(const float* pos_ids, int n, int T, int P, int* cu_rows, int* cu_vt,
-                     int* hist_len, int* counts, int* err, hipStream_t s);
+                     int* hist_len, int* counts, int* err, AttnSeq* seqs, hipStream_t s);
+hipError_t prefix_tables(const uint16_t* rows_in, long stride_in, int m_max, int H, const int* counts,
+                         const int* lens, const int* offs, int n, int S, int cap, uint16_t* seq, int* row_req,
+                         int* row_pos, int* c_rows, int* vt_col, AttnSeq* seqs, hipStream_t s);
+hipError_t active_tables(const int* lens, int n, int S, int P, int cap, int* row_req, int* row_pos,
+                         int* c_rows, int* vt_col, AttnSeq* seqs, int* patch_rows, int* lh_rows,
+                         hipStream_t s);
+hipError_t cache_advance(int* lens, const int* counts, int n, hipStream_t s);
 hipError_t fm_gather(const uint16_t* inp, int n, int T, int P, int H, const int* cu_rows,
                      const int* cu_vt, const int* hist_len, uint16_t* seq, int* row_req,
                      int* row_pos, int* vt_col, int* patch_rows, hipStream_t s);
@@ -26,6 +35,8 @@ hipError_t unpack_rows(const uint16_t* src, int n, int T, int P, int D, const in
                        const int* hist_len, uint16_t* dst, hipStream_t s);
 hipError_t scatter_rows(const uint16_t* src, const int* rows_idx, int rows, int H, uint16_t* dst,
                         hipStream_t s);
+hipError_t gather_rows(const uint16_t* src, const int* src_rows, const int* dst_rows, int rows, int H,
+                       uint16_t* dst, hipStream_t s);
 hipError_t z_update(uint16_t* z, const uint16_t* v, float dt, long n, hipStream_t s);
 
 }  // namespace dfh

@@ -172,7 +172,7 @@ __device__ __forceinline__ void run_epilogue(const GemmArgs& a, ACC (&acc)[C::RN
             }
           }
           if (valid) {
-            uint16_t* cp = a.C + (long)m * a.ldc + nb;
+            uint16_t* cp = a.C + (long)(a.c_rows ? a.c_rows[m] : m) * a.ldc + nb;
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
               const int d = 8 * g + 4 * hi;

@@ -69,7 +69,7 @@ ln_modulate_kernel(const uint16_t* __restrict__ x, long ldx, uint16_t* __restric
 __global__ void __launch_bounds__(1024)
 fm_layout_kernel(const float* __restrict__ pos_ids, int n, int T, int P, int* __restrict__ cu_rows,
                  int* __restrict__ cu_vt, int* __restrict__ hist_len, int* __restrict__ counts,
-                 int* __restrict__ err) {
+                 int* __restrict__ err, AttnSeq* __restrict__ seqs) {
   __shared__ int s_rows[1024], s_vt[1024];
   const int i = threadIdx.x;
   int c = 0;
@@ -98,6 +98,9 @@ fm_layout_kernel(const float* __restrict__ pos_ids, int n, int T, int P, int* __
   if (i < n) {
     cu_rows[i + 1] = s_rows[i];
     cu_vt[i + 1] = s_vt[i];
+    // request i: rows [r0, r0 + c + P); history causal below c - 1
+    const int r0 = s_rows[i] - Ti, v0 = s_vt[i] - ((Ti + 7) & ~7);
+    seqs[i] = AttnSeq{r0, r0, v0, 0, Ti, c - 1, Ti, r0};
   }
   if (i == 0) {
     cu_rows[0] = 0;
@@ -218,6 +221,18 @@ __global__ void scatter_rows_kernel(const uint16_t* __restrict__ src, const int*
     *reinterpret_cast<uint4*>(dp + col) = *reinterpret_cast<const uint4*>(sp + col);
 }
 
+// dst[dst_rows[r]] = src[src_rows ? src_rows[r] : r]   (rows of H bf16)
+__global__ void gather_rows_kernel(const uint16_t* __restrict__ src, const int* __restrict__ src_rows,
+                                   const int* __restrict__ dst_rows, int rows, int H, uint16_t* __restrict__ dst) {
+  const int lane = threadIdx.x & 63;
+  const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (r >= rows) return;
+  const uint16_t* sp = src + (long)(src_rows ? src_rows[r] : r) * H;
+  uint16_t* dp = dst + (long)dst_rows[r] * H;
+  for (int col = lane * 8; col < H; col += 64 * 8)
+    *reinterpret_cast<uint4*>(dp + col) = *reinterpret_cast<const uint4*>(sp + col);
+}
+
 // z = bf16(z + bf16(v * dt))  (batched_fm.py:125 in bf16)
 __global__ void z_update_kernel(uint16_t* __restrict__ z, const uint16_t* __restrict__ v, float dt,
                                 long n) {
@@ -225,7 +240,100 @@ __global__ void z_update_kernel(uint16_t* __restrict__ z, const uint16_t* __rest
   if (i < n) z[i] = f2bf(bf2f(z[i]) + rbf(bf2f(v[i]) * dt));
 }
 
+// ---------------------------------------------------------------------------
+// Prefix-cache pass tables. Rows of a pass are ordered (timestep k, stream i,
+// row r): pass row = k * Mtot + offs[i] + r with Mtot = offs[n]. Stream i's new
+// rows r < counts[i] take positions lens[i] + r and land in slab region
+// (k, i) = rows/columns [(k*n + i) * cap, +cap). One wave per padded input row.
+__global__ void __launch_bounds__(256)
+prefix_tables_kernel(const uint16_t* __restrict__ rows_in, long stride_in, int m_max, int H,
+                     const int* __restrict__ counts, const int* __restrict__ lens,
+                     const int* __restrict__ offs, int n, int S, int cap, uint16_t* __restrict__ seq,
+                     int* __restrict__ row_req, int* __restrict__ row_pos, int* __restrict__ c_rows,
+                     int* __restrict__ vt_col, AttnSeq* __restrict__ seqs) {
+  const int lane = threadIdx.x & 63;
+  const long pr = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (pr >= (long)S * n * m_max) return;
+  const int k = (int)(pr / ((long)n * m_max));
+  const int i = (int)((pr / m_max) % n);
+  const int r = (int)(pr % m_max);
+  const int Mtot = offs[n];
+  const int len = lens[i], cnt = counts[i];
+  const int base = (k * n + i) * cap;
+  if (r == 0 && lane == 0)
+    seqs[k * n + i] = AttnSeq{base, base, base, len, len + cnt, len + cnt, len + cnt, k * Mtot + offs[i] - len};
+  if (r >= cnt) return;
+  const int row = k * Mtot + offs[i] + r;
+  if (lane == 0) {
+    row_req[row] = k * n + i;
+    row_pos[row] = len + r;
+    c_rows[row] = base + len + r;
+    vt_col[row] = base + len + r;
+  }
+  const uint16_t* sp = rows_in + (long)i * stride_in + (long)r * H;
+  uint16_t* dp = seq + (long)row * H;
+  for (int col = lane * 8; col < H; col += 64 * 8)
+    *reinterpret_cast<uint4*>(dp + col) = *reinterpret_cast<const uint4*>(sp + col);
+}
+
+// Active-pass tables for all S steps: rows (k, i, j), j = 0 the last hidden row
+// (position lens[i]), j = 1..P the latent rows; queries of stream i at step k
+// are the rows lens[i] .. lens[i] + P of region (k, i), which they all see.
+__global__ void active_tables_kernel(const int* __restrict__ lens, int n, int S, int P, int cap,
+                                     int* __restrict__ row_req, int* __restrict__ row_pos,
+                                     int* __restrict__ c_rows, int* __restrict__ vt_col,
+                                     AttnSeq* __restrict__ seqs, int* __restrict__ patch_rows,
+                                     int* __restrict__ lh_rows) {
+  const int R = 1 + P;
+  const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= S * n * R) return;
+  const int k = idx / (n * R), i = (idx / R) % n, j = idx % R;
+  const int len = lens[i];
+  const int base = (k * n + i) * cap;
+  row_req[idx] = k * n + i;
+  row_pos[idx] = len + j;
+  c_rows[idx] = base + len + j;
+  vt_col[idx] = base + len + j;
+  if (j == 0) seqs[k * n + i] = AttnSeq{base, base, base, len, len + R, 0, len + R, i * R - len};
+  if (k == 0) {
+    if (j == 0) lh_rows[i] = i * R;
+    else patch_rows[i * P + j - 1] = i * R + j;
+  }
+}
+
+// lens[i] += counts[i]; offs = exclusive prefix sum of counts (offs[n] = total)
+__global__ void cache_advance_kernel(int* __restrict__ lens, const int* __restrict__ counts, int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) lens[i] += counts[i];
+}
+
 }  // namespace
+
+hipError_t prefix_tables(const uint16_t* rows_in, long stride_in, int m_max, int H, const int* counts,
+                         const int* lens, const int* offs, int n, int S, int cap, uint16_t* seq, int* row_req,
+                         int* row_pos, int* c_rows, int* vt_col, AttnSeq* seqs, hipStream_t s) {
+  const long rows = (long)S * n * m_max;
+  if (rows <= 0) return hipSuccess;
+  if (H % 8) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(prefix_tables_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, s, rows_in,
+                     stride_in, m_max, H, counts, lens, offs, n, S, cap, seq, row_req, row_pos, c_rows, vt_col,
+                     seqs);
+  return hipGetLastError();
+}
+
+hipError_t active_tables(const int* lens, int n, int S, int P, int cap, int* row_req, int* row_pos,
+                         int* c_rows, int* vt_col, AttnSeq* seqs, int* patch_rows, int* lh_rows,
+                         hipStream_t s) {
+  const int total = S * n * (1 + P);
+  hipLaunchKernelGGL(active_tables_kernel, dim3((total + 255) / 256), dim3(256), 0, s, lens, n, S, P, cap,
+                     row_req, row_pos, c_rows, vt_col, seqs, patch_rows, lh_rows);
+  return hipGetLastError();
+}
+
+hipError_t cache_advance(int* lens, const int* counts, int n, hipStream_t s) {
+  hipLaunchKernelGGL(cache_advance_kernel, dim3((n + 255) / 256), dim3(256), 0, s, lens, counts, n);
+  return hipGetLastError();
+}
 
 hipError_t ln_modulate(const uint16_t* x, long ldx, uint16_t* out, long ldo, const uint16_t* shift,
                        const uint16_t* scale, long ld_mod, const int* row_req, const int* row_map,
@@ -252,10 +360,10 @@ hipError_t ln_modulate(const uint16_t* x, long ldx, uint16_t* out, long ldo, con
 }
 
 hipError_t fm_layout(const float* pos_ids, int n, int T, int P, int* cu_rows, int* cu_vt,
-                     int* hist_len, int* counts, int* err, hipStream_t s) {
+                     int* hist_len, int* counts, int* err, AttnSeq* seqs, hipStream_t s) {
   if (n <= 0 || n > 1024) return hipErrorInvalidValue;
   hipLaunchKernelGGL(fm_layout_kernel, dim3(1), dim3(1024), 0, s, pos_ids, n, T, P, cu_rows, cu_vt,
-                     hist_len, counts, err);
+                     hist_len, counts, err, seqs);
   return hipGetLastError();
 }
 
@@ -302,6 +410,15 @@ hipError_t scatter_rows(const uint16_t* src, const int* rows_idx, int rows, int 
   if (H % 8 != 0) return hipErrorInvalidValue;
   hipLaunchKernelGGL(scatter_rows_kernel, dim3((rows + 3) / 4), dim3(256), 0, s, src, rows_idx, rows,
                      H, dst);
+  return hipGetLastError();
+}
+
+hipError_t gather_rows(const uint16_t* src, const int* src_rows, const int* dst_rows, int rows, int H,
+                       uint16_t* dst, hipStream_t s) {
+  if (rows <= 0) return hipSuccess;
+  if (H % 8 != 0) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(gather_rows_kernel, dim3((rows + 3) / 4), dim3(256), 0, s, src, src_rows, dst_rows, rows, H,
+                     dst);
   return hipGetLastError();
 }
 

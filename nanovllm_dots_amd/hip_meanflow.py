@@ -361,3 +361,71 @@ def batched_meanflow(core, *, input_sequence, attn_mask, pos_ids, g_cond, num_st
         vt = vfp(x=z_c, timesteps=t, duration=dt, attn_mask=attn_mask, pos_ids=pos_ids, g_cond=g_cond)
         z = z + vt[:, latent_start:] * dt.view(-1, 1, 1)
     return z
+
+
+class HipFMCache:
+    """Prefix K/V cache + cached MeanFlow solve for ``n_streams`` streams.
+
+    The MeanFlow counterpart of the reference's per-timestep FM cache
+    (nanovllm_dots/models/dots/cached_fm.py:82-197, written there for the CFG
+    flow-matching DiT): ``extend`` appends history rows to every stream's
+    prefix at all ``num_steps`` timesteps in one batched pass; ``solve`` runs the
+    NFE-step solve of the active rows (last hidden row + latent patch) against
+    the cache, equal to a full-recompute solve of prefix + last hidden row.
+    """
+
+    def __init__(self, head: HipFMHead, n_streams: int, capacity: int, num_steps: int = 4):
+        self.head = head
+        self.lib = head.lib
+        self.n = n_streams
+        self.nfe = num_steps
+        h = _lib.vp()
+        _lib.check(self.lib.dfh_kvcache_create(head.handle, n_streams, capacity, num_steps, C.byref(h)),
+                   "dfh_kvcache_create")
+        self.cache = h
+        ts, dts = meanflow_grid(num_steps)
+        self._tg = (C.c_float * num_steps)(*ts)
+        self._dg = (C.c_float * num_steps)(*dts)
+
+    @property
+    def lengths(self) -> list[int]:
+        arr = (C.c_int * self.n)()
+        _lib.check(self.lib.dfh_kvcache_lengths(self.cache, arr), "dfh_kvcache_lengths")
+        return list(arr)
+
+    def reset(self) -> None:
+        _lib.check(self.lib.dfh_kvcache_reset(self.cache, _lib.stream_ptr()), "dfh_kvcache_reset")
+
+    def extend(self, rows: torch.Tensor, counts, g_cond=None) -> None:
+        """rows: [n, m_max, H] (FM sequence space); counts[i] rows of stream i."""
+        s = self.head.spec
+        if rows.dim() != 3 or rows.shape[0] != self.n or rows.shape[2] != s.hidden:
+            raise RuntimeError(f"rows must be [{self.n}, m, {s.hidden}], got {tuple(rows.shape)}")
+        r = rows.to(torch.bfloat16).contiguous()
+        g = g_cond.to(torch.bfloat16).contiguous() if g_cond is not None else None
+        cnt = (C.c_int * self.n)(*[int(x) for x in counts])
+        _lib.check(self.lib.dfh_kvcache_extend(self.cache, _lib.ptr(r), r.shape[1], cnt, _lib.ptr(g),
+                                               self._tg, self._dg, _lib.stream_ptr()), "dfh_kvcache_extend")
+
+    def solve(self, last_hidden: torch.Tensor, g_cond=None, noise=None) -> torch.Tensor:
+        s = self.head.spec
+        lh = last_hidden.reshape(self.n, s.hidden).to(torch.bfloat16).contiguous()
+        if noise is None:
+            noise = torch.randn((self.n, s.patch, s.latent_dim), device=lh.device, dtype=torch.bfloat16)
+        nz = noise.to(torch.bfloat16).contiguous()
+        g = g_cond.to(torch.bfloat16).contiguous() if g_cond is not None else None
+        out = torch.empty((self.n, s.patch, s.latent_dim), device=lh.device, dtype=torch.bfloat16)
+        _lib.check(self.lib.dfh_kvcache_solve(self.cache, _lib.ptr(lh), _lib.ptr(g), _lib.ptr(nz), _lib.ptr(out),
+                                              self._tg, self._dg, _lib.stream_ptr()), "dfh_kvcache_solve")
+        return out
+
+    def close(self) -> None:
+        if getattr(self, "cache", None):
+            self.lib.dfh_kvcache_destroy(self.cache)
+            self.cache = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

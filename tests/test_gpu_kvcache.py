@@ -1,0 +1,111 @@
+"""Cached MeanFlow solve (prefix K/V cache) vs full recompute. GPU only.
+Tolerance as the full solve: per-row cosine >= 0.9999, max |diff| <= 2% of max |ref|."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import cos_stats
+from oracle import dit_ref as R
+from oracle.kvcache_ref import FMCacheRef
+
+pytestmark = pytest.mark.gpu
+
+CFG = R.DitConfig(hidden=256, heads=4, ffn=1024, n_blocks=2, latent_dim=64, patch=16)
+
+
+def _head(cfg, seed):
+    from nanovllm_dots_amd import FMSpec, HipFMHead
+    W = R.random_dit_weights(cfg, seed)
+    return HipFMHead(FMSpec.of(cfg), W, device="cuda"), R.weights_for_regime(W, "bf16")
+
+
+def _pad(rows_list, H):
+    m = max(1, max(r.shape[0] for r in rows_list))
+    out = torch.zeros(len(rows_list), m, H)
+    for i, r in enumerate(rows_list):
+        out[i, :r.shape[0]] = r
+    return out
+
+
+def _check(got, ref, ld, label):
+    got, ref = got.float().cpu(), ref.float().cpu()
+    cmin, _ = cos_stats(got, ref, ld)
+    err = (got - ref).abs().max().item()
+    print(f"{label}: cos min {cmin:.6f} maxabs {err:.4g}", flush=True)
+    assert cmin >= 0.9999 and err <= 0.02 * ref.abs().max().item()
+
+
+def test_cached_solve_matches_full_recompute_oracle():
+    from nanovllm_dots_amd import HipFMCache
+    head, Wb = _head(CFG, 5)
+    lens, hist, noise = R.synthetic_requests(3, 20, 300, CFG, seed=7)
+    g = R.round_bf16(torch.from_numpy(0.3 * np.random.RandomState(2).standard_normal((3, CFG.hidden)).astype(np.float32)))
+    ref = R.meanflow_solve_varlen(Wb, CFG, hist, g, noise, 4, "bf16")
+    cache = HipFMCache(head, 3, max(lens) + 32, 4)
+    prefix = [h[:-1] for h in hist]
+    cache.extend(_pad(prefix, CFG.hidden).cuda(), [p.shape[0] for p in prefix], g_cond=g.cuda())
+    assert cache.lengths == [L - 1 for L in lens]
+    lh = torch.stack([h[-1] for h in hist]).cuda()
+    got = cache.solve(lh, g_cond=g.cuda(), noise=noise.cuda())
+    _check(got, ref, CFG.latent_dim, "cached-vs-full")
+
+
+def test_cached_solve_matches_cached_oracle_and_incremental_extend():
+    from nanovllm_dots_amd import HipFMCache
+    head, Wb = _head(CFG, 6)
+    lens, hist, noise = R.synthetic_requests(2, 60, 140, CFG, seed=9)
+    cache = HipFMCache(head, 2, 200, 4)
+    split = [h.shape[0] // 3 for h in hist]
+    first = [h[:s] for h, s in zip(hist, split)]
+    second = [h[s:-1] for h, s in zip(hist, split)]
+    cache.extend(_pad(first, CFG.hidden).cuda(), [r.shape[0] for r in first])
+    cache.extend(_pad(second, CFG.hidden).cuda(), [r.shape[0] for r in second])
+    lh = torch.stack([h[-1] for h in hist]).cuda()
+    got = cache.solve(lh, noise=noise.cuda())
+    for i in range(2):
+        ref_cache = FMCacheRef(Wb, CFG, 4, None, "bf16")
+        ref_cache.extend(hist[i][:-1])
+        ref = ref_cache.solve(hist[i][-1], noise[i])
+        _check(got[i], ref, CFG.latent_dim, f"cached-oracle stream {i}")
+
+
+def test_cached_matches_direct_hip_solve():
+    """The cached solve and the direct solve of the same sequences agree."""
+    from nanovllm_dots_amd import HipFMCache, HipMeanflow
+    head, _ = _head(CFG, 8)
+    lens, hist, noise = R.synthetic_requests(4, 5, 260, CFG, seed=11)
+    inp, mask, pos, g = R.pack_fm_inputs(hist, CFG.patch, CFG.hidden)
+    bf = lambda t: t.to("cuda", torch.bfloat16)
+    direct = HipMeanflow(None, num_steps=4, dit=object(), head=head)(
+        input_sequence=bf(inp), attn_mask=None, pos_ids=pos.cuda(), g_cond=bf(g), noise=bf(noise))
+    cache = HipFMCache(head, 4, max(lens) + 24, 4)
+    prefix = [h[:-1] for h in hist]
+    cache.extend(_pad(prefix, CFG.hidden).cuda(), [p.shape[0] for p in prefix])
+    got = cache.solve(torch.stack([h[-1] for h in hist]).cuda(), noise=bf(noise))
+    _check(got, direct, CFG.latent_dim, "cached-vs-direct")
+
+
+def test_capacity_overflow_raises():
+    from nanovllm_dots_amd import HipFMCache
+    head, _ = _head(CFG, 1)
+    cache = HipFMCache(head, 1, 40, 4)
+    with pytest.raises(RuntimeError, match="capacity"):
+        cache.extend(torch.zeros(1, 30, CFG.hidden).cuda(), [30])
+    cache.extend(torch.zeros(1, 20, CFG.hidden).cuda(), [20])
+    assert cache.lengths == [20]
+
+
+def test_full_size_long_prefix():
+    """12 blocks, H=1024; two streams with 2,000-row prefixes, cached vs oracle full recompute."""
+    from nanovllm_dots_amd import HipFMCache
+    cfg = R.DitConfig(hidden=1024, heads=16, ffn=4096, n_blocks=12, latent_dim=64, patch=16)
+    head, Wb = _head(cfg, 2)
+    lens, hist, noise = R.synthetic_requests(2, 2000, 2000, cfg, seed=12)
+    ref = R.meanflow_solve_varlen(Wb, cfg, hist, None, noise, 4, "bf16")
+    cache = HipFMCache(head, 2, 2048, 4)
+    prefix = [h[:-1] for h in hist]
+    cache.extend(_pad(prefix, cfg.hidden).cuda(), [p.shape[0] for p in prefix])
+    got = cache.solve(torch.stack([h[-1] for h in hist]).cuda(), noise=noise.cuda())
+    _check(got, ref, cfg.latent_dim, "full-size cached")
