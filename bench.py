@@ -106,6 +106,58 @@ def w8a8_bench(reps: int = 20):
     return out
 
 
+def kvcache_bench(head, cfg, reps: int = 10):
+    """Long-audio cached solve: 4 streams, each with a cached prefix of 600 prior
+    patches x 16 rows + 512 context rows (the last of them is the active block's
+    hidden row), full 12-block DiT, NFE=4. Returns timings, xRT and the decode
+    attention's HBM rate over the cached K/V."""
+    import numpy as np
+    import torch
+    from nanovllm_dots_amd import HipFMCache
+    n, rows = 4, 600 * 16 + 512
+    L = rows - 1
+    H = cfg.hidden
+    rs = np.random.RandomState(5)
+    hist = torch.from_numpy(rs.standard_normal((n, rows, H)).astype(np.float32)).bfloat16().cuda()
+    noise = torch.from_numpy(rs.standard_normal((n, cfg.patch, cfg.latent_dim)).astype(np.float32)).bfloat16().cuda()
+    cache = HipFMCache(head, n, rows + cfg.patch + 8, 4)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    cache.extend(hist[:, :L], [L] * n)
+    e1.record()
+    torch.cuda.synchronize()
+    prime_ms = e0.elapsed_time(e1)
+    lh = hist[:, L].contiguous()
+    for _ in range(2):
+        out = cache.solve(lh, noise=noise)
+    torch.cuda.synchronize()
+    head.profile(True)
+    head.profile_read()
+    e0.record()
+    for _ in range(reps):
+        out = cache.solve(lh, noise=noise)
+    e1.record()
+    torch.cuda.synchronize()
+    prof = head.profile_read()
+    head.profile(False)
+    assert torch.isfinite(out.float()).all()
+    ms = e0.elapsed_time(e1) / reps
+    attn_ms, attn_n = prof["attention"]
+    kv_bytes_launch = n * 2 * (L + 1 + cfg.patch) * H * 2       # one layer's K and V, all streams
+    gbps = kv_bytes_launch / (attn_ms / attn_n * 1e-3) / 1e9
+    prime_flops = cfg.n_blocks * 2 * (4 * H * H + 2 * H * cfg.ffn) * (4 * n * L)
+    res = {"streams": n, "prefix_rows": L, "nfe": 4, "solve_ms": round(ms, 3),
+           "latent_xRT": round(n * cfg.patch * FRAME_S / (ms * 1e-3), 1),
+           "kv_bytes_per_step": kv_bytes_launch * cfg.n_blocks,
+           "decode_attn_us_per_layer": round(attn_ms / attn_n * 1e3, 2),
+           "decode_attn_GBps": round(gbps, 1), "decode_attn_frac_hbm": round(gbps / PEAK_HBM_GBS, 4),
+           "prime_ms": round(prime_ms, 2), "prime_tflops": round(prime_flops / (prime_ms * 1e-3) / 1e12, 1)}
+    log(f"kvcache: {res}")
+    cache.close()
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -116,6 +168,9 @@ def main():
     ap.add_argument("--cpu-budget", type=float, default=20.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-w8a8", action="store_true")
+    ap.add_argument("--no-kvcache", action="store_true")
+    ap.add_argument("--calib-copy-mib", type=int, default=0,
+                    help="run a device copy of this size first (HBM counter calibration under rocprofv3)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the FM head shards requests across GPUs with no "
@@ -129,6 +184,13 @@ def main():
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.calib_copy_mib:
+        src = torch.empty(args.calib_copy_mib << 20, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     cfg = R.DitConfig(hidden=1024, heads=16, ffn=4096, n_blocks=12, latent_dim=64, patch=16)
     log("generating weights / inputs")
     W = R.random_dit_weights(cfg, args.seed)
@@ -189,6 +251,7 @@ def main():
     log("per-class ms/solve: " + ", ".join(f"{k}={v['ms_per_solve']:.3f}" for k, v in breakdown.items()))
 
     w8 = None if args.no_w8a8 else w8a8_bench()
+    kvc = None if args.no_kvcache else kvcache_bench(head, cfg)
 
     cpu = None
     if not args.no_cpu:
@@ -214,6 +277,7 @@ def main():
                      "avg_launch_ms": round(avg_ms, 5), "flops_per_launch": per_launch[dom]},
         "kernel_breakdown": breakdown,
         "w8a8_m16384": w8,
+        "kvcache_4x10111": kvc,
         "cpu_baseline": ({k: (round(v, 5) if isinstance(v, float) else v) for k, v in cpu.items()
                           if k in ("value", "unit", "cores", "kind", "sample")} if cpu else None),
         "cpu_xRT": round(cpu["xRT"], 4) if cpu else None,

@@ -542,7 +542,7 @@ int dfh_meanflow_solve(DfhHandle* h, const DfhSolveArgs* a, void* stream) {
   if (!a->input_sequence || !a->pos_ids || !a->noise || !a->out || !a->t_grid || !a->dt_grid)
     return fail("dfh_meanflow_solve: a required pointer is NULL");
   if (!c.meanflow) return fail("dfh_meanflow_solve: DiT has no duration embedder (not MeanFlow)");
-  if ((long)n * T * 4 * c.ffn >= (1L << 31))
+  if ((long)n * T * (c.ffn > 2 * c.hidden ? c.ffn : 2 * c.hidden) >= (1L << 31))
     return fail("dfh_meanflow_solve: n*T too large for 32-bit offsets");
   if (reserve(h, n, T, S, s)) return 1;
   const int H = c.hidden, Pp = c.patch, ld = c.latent_dim;
@@ -583,7 +583,7 @@ int dfh_dit_forward(DfhHandle* h, const DfhForwardArgs* a, void* stream) {
   const int n = a->n, T = a->total_len;
   if (n <= 0 || n > 1024 || T <= c.patch) return fail("dfh_dit_forward: bad shape n=%d T=%d", n, T);
   if (!a->x || !a->timesteps || !a->pos_ids || !a->out) return fail("dfh_dit_forward: NULL pointer");
-  if ((long)n * T * 4 * c.ffn >= (1L << 31)) return fail("dfh_dit_forward: n*T too large");
+  if ((long)n * T * (c.ffn > 2 * c.hidden ? c.ffn : 2 * c.hidden) >= (1L << 31)) return fail("dfh_dit_forward: n*T too large");
   if (reserve(h, n, T, 1, s)) return 1;
   const int H = c.hidden, Pp = c.patch, ld = c.latent_dim;
   if (layout(h, n, T, a->pos_ids, a->x, s)) return 1;
@@ -765,7 +765,8 @@ int cache_extend_dev(DfhKVCache* c, const uint16_t* rows, long stride, int m_max
   const DfhConfig& cf = h->cfg;
   const long total = (long)c->S * Mtot;
   if (total == 0) return 0;
-  if (total * 4L * cf.ffn >= (1L << 31)) return fail("kv cache extend: %ld rows too many for one pass", total);
+  if (total * (cf.ffn > 2 * cf.hidden ? cf.ffn : 2 * cf.hidden) >= (1L << 31))
+    return fail("kv cache extend: %ld rows too many for one pass (32-bit element offsets)", total);
   if (reserve(h, c->n, c->cap, c->S, s)) return 1;  // RoPE positions up to cap
   if (reserve_rows(h, total, s)) return 1;
   if (cache_tables(c, total, s)) return 1;
