@@ -32,8 +32,24 @@ PEAK_INT8_TOPS = 5000.0        # MI355X dense int8 MFMA
 FRAME_S = 0.04                 # one latent frame = 1920 samples at 48 kHz
 
 
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "pmc_hbm_traffic_dit_kernels_meanflow_nfe4_64req.md")
+
+
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
+
+
+def pmc_traffic(role: str):
+    """HBM bytes per launch of ``role`` from the committed FETCH_SIZE/WRITE_SIZE
+    summary of this workload (two rocprofv3 --pmc runs, copy-calibrated), or None."""
+    try:
+        for line in open(TRAFFIC_PROFILE):
+            f = line.split()
+            if len(f) == 3 and f[0] == "traffic_bytes_per_launch" and f[1] == role:
+                return int(f[2])
+    except OSError:
+        pass
+    return None
 
 
 def cpu_baseline(cfg, W, lens, hist, noise, budget_s: float):
@@ -240,6 +256,11 @@ def main():
     H, F = cfg.hidden, cfg.ffn
     per_launch = {"qkv_gemm": 2 * M * H * 3 * H, "o_gemm": 2 * M * H * H,
                   "fc1_gemm": 2 * M * H * F, "fc2_gemm": 2 * M * F * H}
+    # compulsory HBM bytes per launch: A, W, outputs (+ residual read for gate-residual)
+    algo_bytes = {"qkv_gemm": 2 * (M * H + 3 * H * H + 3 * M * H),
+                  "o_gemm": 2 * (M * H + H * H + 2 * M * H),
+                  "fc1_gemm": 2 * (M * H + F * H + M * F),
+                  "fc2_gemm": 2 * (M * F + F * H + 2 * M * H)}
     classes = {k: v for k, v in prof.items()}
     dom = max(per_launch, key=lambda k: classes[k][0])
     dom_ms, dom_n = classes[dom]
@@ -273,7 +294,8 @@ def main():
         "gemm_only_tflops": round(gemm_flops / (gemm_ms * 1e-3) / 1e12, 2) if gemm_ms > 0 else None,
         "roofline": {"bound": "mfma", "kernel": dom, "achieved": round(achieved, 2),
                      "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": None,
+                     "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": pmc_traffic(dom),
+                     "traffic_unit": "bytes/launch", "algorithmic_bytes": algo_bytes[dom],
                      "avg_launch_ms": round(avg_ms, 5), "flops_per_launch": per_launch[dom]},
         "kernel_breakdown": breakdown,
         "w8a8_m16384": w8,
