@@ -11,13 +11,25 @@
 // is all-causal from a nonzero q_begin. No mask tensor is read.
 // softmax(q k^T / 8) v with an online (flash) softmax.
 //
-// Work split: one workgroup = 128 query rows of one (request, head); wave w owns
-// 32 rows. Per 64-key tile the wave computes S^T = K Q^T (32 keys x 32 queries
-// per MFMA block): a lane then holds 32 key scores of ONE query, so the row
-// max/sum need a single cross-lane exchange (lane ^ 32), and the probabilities
-// are already in the B-operand layout of O^T += V^T P^T. V arrives transposed
-// (V^T [H, tokens], written by the QKV GEMM epilogue) so its A-operand
-// fragments are contiguous LDS reads.
+// Work split: one workgroup = 128 query rows of one (sequence, head); wave w
+// owns 32 of them. Workgroups are numbered so that every query tile of one
+// (sequence, head) runs on the same XCD (workgroup i goes to XCD i % 8), where
+// the K/V tiles they share stay in that XCD's L2; (sequence, head) pairs are
+// dealt round-robin over the XCDs and each pair's longest query tiles come first.
+//
+// Per 64-key tile, K and V^T arrive by global->LDS DMA into double-buffered,
+// XOR-swizzled tiles (16-B chunk c of row r at slot c ^ ((r >> 1) & 7), which
+// keeps the 32-row fragment reads conflict-free). The wave computes
+// S^T = K Q^T (32 keys x 32 queries per MFMA block), so a lane holds 32 scores
+// of ONE query and the row max needs one cross-lane exchange (lane ^ 32). The
+// K rows feeding the MFMA A operand are read with bits 2 and 3 of the row index
+// swapped; each lane's accumulators then hold 8 CONSECUTIVE keys per P^T k-step,
+// so its V^T operand is one 16-B LDS read. The running max is refreshed only
+// when a row's max grows by more than 2^8 (exact: numerator and denominator
+// share the stale max; p <= 256 is representable in bf16 and f32), and only
+// tiles that cross a row's visible-key limit are masked. exp2 is the hardware
+// v_exp_f32 (results below 2^-126 flush to zero: such weights are below one
+// f32 ulp of the row's largest weight).
 #include "dfh_device.h"
 #include "dfh_kernels.h"
 
@@ -28,20 +40,32 @@ namespace {
 constexpr int BQ = 128;    // query rows per workgroup
 constexpr int BKV = 64;    // keys per tile
 constexpr int HD = 64;     // head dim
-constexpr int LDS_K = HD + 8;    // K tile row: 64 d + pad
-constexpr int LDS_V = BKV + 8;   // V^T tile row: 64 keys + pad
+constexpr int NXCD = 8;
+constexpr float kRescaleLog2 = 8.0f;  // lazy max refresh threshold (log2 units)
 
-__global__ void __launch_bounds__(256, 2)
+typedef float floatx8 __attribute__((ext_vector_type(8)));
+
+// 64 rows x 128 B tile, swizzled 16-B chunks
+__device__ __forceinline__ int att_off(int r, int c) { return r * 64 + ((c ^ ((r >> 1) & 7)) << 3); }
+// row index with bits 2 and 3 swapped
+__device__ __forceinline__ int key_perm(int x) { return (x & ~12) | ((x & 4) << 1) | ((x & 8) >> 1); }
+
+__global__ void __launch_bounds__(256, 3)
 seq_attention_kernel(const uint16_t* __restrict__ qk, long ldqk, const uint16_t* __restrict__ vt,
                      long ld_vt, uint16_t* __restrict__ out, long ldo, const AttnSeq* __restrict__ seqs,
-                     int heads, float scale_log2) {
-  __shared__ __attribute__((aligned(16))) uint16_t Ks[2][BKV * LDS_K];
-  __shared__ __attribute__((aligned(16))) uint16_t Vs[2][HD * LDS_V];
+                     int n_seq, int heads, int nq, float scale_log2) {
+  __shared__ __attribute__((aligned(16))) uint16_t K0[BKV * HD];
+  __shared__ __attribute__((aligned(16))) uint16_t K1[BKV * HD];
+  __shared__ __attribute__((aligned(16))) uint16_t V0[HD * BKV];
+  __shared__ __attribute__((aligned(16))) uint16_t V1[HD * BKV];
 
-  const AttnSeq sq = seqs[blockIdx.z];
-  const int h = blockIdx.y;
-  const int nq = gridDim.x;
-  const int qt = nq - 1 - (int)blockIdx.x;  // longest (last) query tiles first
+  const int xcd = blockIdx.x % NXCD;
+  const int slot = blockIdx.x / NXCD;
+  const int pair = (slot / nq) * NXCD + xcd;
+  if (pair >= n_seq * heads) return;
+  const int qt = nq - 1 - slot % nq;  // longest (last) query tiles first
+  const int h = pair % heads;
+  const AttnSeq sq = seqs[pair / heads];
   const int q0 = sq.q_begin + qt * BQ;
   if (q0 >= sq.q_end) return;
   const int T = sq.kv_len;           // keys of full rows
@@ -51,19 +75,18 @@ seq_attention_kernel(const uint16_t* __restrict__ qk, long ldqk, const uint16_t*
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l32 = lane & 31, hi = lane >> 5;
 
-  // visible keys of query q: [0, q+1) below cend, [0, T) from cend on
+  // visible keys of query q: [0, q+1) below cend, [0, T) from cend on (monotone in q)
   auto limit = [&](int q) { return q < cend ? q + 1 : T; };
-  const int r_last = min(q0 + BQ, sq.q_end) - 1;
-  const int kmax = limit(r_last);  // keys needed by this workgroup (limit is monotone)
+  const int kmax = limit(min(q0 + BQ, sq.q_end) - 1);  // keys this workgroup needs
   const int ntiles = (kmax + BKV - 1) / BKV;
 
-  // this lane's query and its visible-key limit
   const int q = q0 + wave * 32 + l32;
   const int qc = q < sq.q_end ? q : sq.q_end - 1;
   const int lim = limit(qc);
-  // keys needed by this wave
   const int wq_first = q0 + wave * 32;
-  const int wave_kmax = wq_first >= sq.q_end ? 0 : limit(min(wq_first + 31, sq.q_end - 1));
+  const bool wave_on = wq_first < sq.q_end;
+  const int wave_kmax = wave_on ? limit(min(wq_first + 31, sq.q_end - 1)) : 0;  // keys any lane sees
+  const int wave_kall = wave_on ? limit(wq_first) : 0;                          // keys every lane sees
 
   // Q fragments (B operand): Q[q][16*kk + 8*hi .. +8]
   bf16x8 qf[4];
@@ -73,26 +96,21 @@ seq_attention_kernel(const uint16_t* __restrict__ qk, long ldqk, const uint16_t*
     for (int kk = 0; kk < 4; ++kk) qf[kk] = *reinterpret_cast<const bf16x8*>(qp + 16 * kk);
   }
 
-  // cooperative tile loads: K tile 64 keys x 128 B, V^T tile 64 d x 128 B; 2+2 chunks/thread
-  auto load_tile = [&](int t, uint4* rk, uint4* rv) {
-    const int k0 = t * BKV;
+  // DMA: wave w, load j covers tile rows [(4j + w) * 8, +8); lane -> row + lane/8, slot lane%8
+  const int dma_r0 = wave * 8 + (lane >> 3);
+  const int dma_c = lane & 7;
+  const uint16_t* kbase = qk + (long)sq.kv_row0 * ldqk + H + h * HD;
+  const uint16_t* vbase = vt + (long)(h * HD) * ld_vt + sq.vt_col0;
+  auto dma = [&](uint16_t* kd, uint16_t* vd, int k0) {
 #pragma unroll
-    for (int cc = 0; cc < 2; ++cc) {
-      const int idx = tid + cc * 256;
-      const int r = idx >> 3, col = (idx & 7) * 8;
-      int key = k0 + r;
-      key = key < T ? key : T - 1;
-      rk[cc] = *reinterpret_cast<const uint4*>(qk + (long)(sq.kv_row0 + key) * ldqk + H + h * HD + col);
-      rv[cc] = *reinterpret_cast<const uint4*>(vt + (long)(h * HD + r) * ld_vt + sq.vt_col0 + k0 + col);
-    }
-  };
-  auto store_tile = [&](int buf, const uint4* rk, const uint4* rv) {
-#pragma unroll
-    for (int cc = 0; cc < 2; ++cc) {
-      const int idx = tid + cc * 256;
-      const int r = idx >> 3, col = (idx & 7) * 8;
-      *reinterpret_cast<uint4*>(&Ks[buf][r * LDS_K + col]) = rk[cc];
-      *reinterpret_cast<uint4*>(&Vs[buf][r * LDS_V + col]) = rv[cc];
+    for (int j = 0; j < 2; ++j) {
+      const int r = j * 32 + dma_r0;
+      const int c = dma_c ^ ((r >> 1) & 7);
+      const int key = min(k0 + r, T - 1);
+      __builtin_amdgcn_global_load_lds(DFH_GPTR(kbase + (long)key * ldqk + c * 8),
+                                       DFH_LPTR(kd + (j * 32 + wave * 8) * 64), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(DFH_GPTR(vbase + (long)r * ld_vt + k0 + c * 8),
+                                       DFH_LPTR(vd + (j * 32 + wave * 8) * 64), 16, 0, 0);
     }
   };
 
@@ -102,81 +120,87 @@ seq_attention_kernel(const uint16_t* __restrict__ qk, long ldqk, const uint16_t*
 #pragma unroll
     for (int v = 0; v < 16; ++v) o[b][v] = 0.f;
   float m_run = -INFINITY, l_run = 0.f;
+  const float thr = kRescaleLog2 / scale_log2;  // in raw score units
+  const int krow = key_perm(l32);
 
-  uint4 rk[2], rv[2];
-  load_tile(0, rk, rv);
-  store_tile(0, rk, rv);
-  __syncthreads();
-
-  for (int t = 0; t < ntiles; ++t) {
-    const int cur = t & 1;
-    if (t + 1 < ntiles) load_tile(t + 1, rk, rv);
-    const int k0 = t * BKV;
-    if (k0 < wave_kmax) {
-      // S^T blocks: keys k0 + 32*kb + (8*(v/4) + 4*hi + v%4), query = q
-      floatx16 s[2];
+  auto compute = [&](const uint16_t* Ks, const uint16_t* Vs, int k0) {
+    if (k0 >= wave_kmax) return;  // wave-uniform
+    floatx16 s[2];
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
+    for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
-        for (int v = 0; v < 16; ++v) s[kb][v] = 0.f;
-        const uint16_t* kp = &Ks[cur][(kb * 32 + l32) * LDS_K + 8 * hi];
+      for (int v = 0; v < 16; ++v) s[kb][v] = 0.f;
 #pragma unroll
-        for (int kk = 0; kk < 4; ++kk) {
-          bf16x8 kf = *reinterpret_cast<const bf16x8*>(kp + 16 * kk);
-          s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[kk], s[kb], 0, 0, 0);
-        }
+      for (int kk = 0; kk < 4; ++kk) {
+        const bf16x8 kf = *reinterpret_cast<const bf16x8*>(Ks + att_off(kb * 32 + krow, 2 * kk + hi));
+        s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[kk], s[kb], 0, 0, 0);
       }
-      // mask + running max
-      float mx = -INFINITY;
+    }
+    // accumulator v of block kb holds key k0 + kb*32 + 16*(v/8) + 8*hi + v%8
+    if (k0 + BKV > wave_kall) {
+      const int rel = lim - k0 - 8 * hi;
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          const int key = k0 + kb * 32 + 8 * (v >> 2) + 4 * hi + (v & 3);
-          const float sv = key < lim ? s[kb][v] * scale_log2 : -INFINITY;
-          s[kb][v] = sv;
-          mx = fmaxf(mx, sv);
-        }
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        for (int v = 0; v < 16; ++v)
+          if (kb * 32 + 16 * (v >> 3) + (v & 7) >= rel) s[kb][v] = -INFINITY;
+    }
+    float mx = fmaxf(s[0][0], s[0][1]);
+#pragma unroll
+    for (int v = 2; v < 16; ++v) mx = fmaxf(mx, s[0][v]);
+#pragma unroll
+    for (int v = 0; v < 16; ++v) mx = fmaxf(mx, s[1][v]);
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    if (__any(mx > m_run + thr)) {
       const float m_new = fmaxf(m_run, mx);
-      const float alpha = exp2f(m_run - m_new);
+      const float alpha = __builtin_amdgcn_exp2f((m_run - m_new) * scale_log2);
       m_run = m_new;
-      float psum = 0.f;
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          const float p = exp2f(s[kb][v] - m_new);
-          s[kb][v] = p;
-          psum += p;
-        }
-      l_run = l_run * alpha + psum;
+      l_run *= alpha;
 #pragma unroll
       for (int b = 0; b < 2; ++b)
 #pragma unroll
         for (int v = 0; v < 16; ++v) o[b][v] *= alpha;
-      // O^T[d][q] += V^T[d][keys] P^T[keys][q]; k-step (kb, half) covers keys
-      // kb*32 + 16*half + [0,16): lane holds 8*(v/4) + 4*hi + v%4 for v in [8half, 8half+8)
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int half = 0; half < 2; ++half) {
-          bf16x8 pf;
-#pragma unroll
-          for (int j = 0; j < 8; ++j) pf[j] = (__bf16)s[kb][8 * half + j];
-#pragma unroll
-          for (int db = 0; db < 2; ++db) {
-            const uint16_t* vp = &Vs[cur][(db * 32 + l32) * LDS_V + kb * 32 + 16 * half + 4 * hi];
-            uint2 lo = *reinterpret_cast<const uint2*>(vp);
-            uint2 up = *reinterpret_cast<const uint2*>(vp + 8);
-            uint4 u = make_uint4(lo.x, lo.y, up.x, up.y);
-            bf16x8 vf = *reinterpret_cast<bf16x8*>(&u);
-            o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf, o[db], 0, 0, 0);
-          }
-        }
     }
-    if (t + 1 < ntiles) store_tile(cur ^ 1, rk, rv);
-    __syncthreads();
+    const float mb = m_run * scale_log2;
+    float psum = 0.f;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kb][v], scale_log2, -mb));
+        s[kb][v] = p;
+        psum += p;
+      }
+    l_run += psum;
+    // O^T[d][q] += V^T[d][keys] P^T[keys][q]; k-step (kb, half) = keys kb*32 + 16*half + [0, 16)
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+        floatx8 pv;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) pv[j] = s[kb][8 * half + j];
+        const bf16x8 pf = __builtin_convertvector(pv, bf16x8);
+#pragma unroll
+        for (int db = 0; db < 2; ++db) {
+          const bf16x8 vf =
+              *reinterpret_cast<const bf16x8*>(Vs + att_off(db * 32 + l32, 4 * kb + 2 * half + hi));
+          o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf, o[db], 0, 0, 0);
+        }
+      }
+  };
+
+  dma(K0, V0, 0);
+  for (int t = 0; t < ntiles; t += 2) {
+    wait_vm_lgkm0<0>();
+    __builtin_amdgcn_s_barrier();
+    if (t + 1 < ntiles) dma(K1, V1, (t + 1) * BKV);
+    compute(K0, V0, t * BKV);
+    if (t + 1 >= ntiles) break;
+    wait_vm_lgkm0<0>();
+    __builtin_amdgcn_s_barrier();
+    if (t + 2 < ntiles) dma(K0, V0, (t + 2) * BKV);
+    compute(K1, V1, (t + 1) * BKV);
   }
 
   const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
@@ -356,9 +380,12 @@ hipError_t seq_attention(const uint16_t* qk, long ldqk, const uint16_t* vt, long
                          long ldo, const AttnSeq* seqs, int n_seq, int heads, int max_q, hipStream_t s) {
   if (n_seq <= 0 || max_q <= 0) return hipSuccess;
   const float scale_log2 = 0.125f * 1.4426950408889634f;  // head_dim^-0.5 * log2(e)
-  dim3 grid((max_q + BQ - 1) / BQ, heads, n_seq);
-  dfh_launch(seq_attention_kernel, grid, dim3(256), 0, s, qk, ldqk, vt, ld_vt, out, ldo, seqs, heads,
-             scale_log2);
+  const int nq = (max_q + BQ - 1) / BQ;
+  const long pairs = (long)n_seq * heads;
+  const long grid = (pairs + NXCD - 1) / NXCD * NXCD * nq;
+  if (grid > 0x7fffffffL) return hipErrorInvalidValue;
+  dfh_launch(seq_attention_kernel, dim3((unsigned)grid), dim3(256), 0, s, qk, ldqk, vt, ld_vt, out, ldo, seqs,
+             n_seq, heads, nq, scale_log2);
   return hipGetLastError();
 }
 

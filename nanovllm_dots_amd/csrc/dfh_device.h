@@ -13,6 +13,17 @@ typedef int intx16 __attribute__((ext_vector_type(16)));
 
 #define DFH_WAVE 64
 
+// global / LDS address-space casts for __builtin_amdgcn_global_load_lds
+#define DFH_GPTR(p) ((__attribute__((address_space(1))) void*)(p))
+#define DFH_LPTR(p) ((__attribute__((address_space(3))) void*)(p))
+
+// s_waitcnt vmcnt(n) lgkmcnt(0) (gfx9 encoding: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt_hi[15:14])
+template <int N>
+__device__ __forceinline__ void wait_vm_lgkm0() {
+  static_assert(N >= 0 && N < 64, "vmcnt");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (0 << 8) | ((N >> 4) << 14));
+}
+
 // float32 multiply / add that the compiler may not fuse into an FMA: sequences
 // that reproduce torch's separately rounded elementwise ops use these.
 __device__ __forceinline__ float mul_rn(float a, float b) {

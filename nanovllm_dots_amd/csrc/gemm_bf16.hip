@@ -26,8 +26,6 @@ namespace dfh {
 
 namespace {
 
-#define DFH_GPTR(p) ((__attribute__((address_space(1))) void*)(p))
-#define DFH_LPTR(p) ((__attribute__((address_space(3))) void*)(p))
 
 template <int BM_, int BN_, int BK_, int ST_, int WM_, int WN_>
 struct Cfg {
@@ -84,12 +82,6 @@ struct OpI8 {
   }
 };
 
-// s_waitcnt vmcnt(n) lgkmcnt(0) (gfx9 encoding: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt_hi[15:14])
-template <int N>
-__device__ __forceinline__ void wait_vm_lgkm0() {
-  static_assert(N >= 0 && N < 64, "vmcnt");
-  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (0 << 8) | ((N >> 4) << 14));
-}
 
 
 
