@@ -56,6 +56,9 @@ struct Cfg {
 // (256 B, 64 banks) at a time; a fragment read gives those lanes 16 consecutive
 // rows at one logical chunk and the swizzle makes their 16-B bank groups
 // (row, slot) -> (row*CH + slot) % 16 all distinct.
+// buffer resource word 3 for gfx9-family raw (stride 0) buffers: 32-bit data format
+constexpr int kBufferFlags = 0x00020000;
+
 template <int CH>
 __device__ __forceinline__ int swz(int row) {
   return CH == 8 ? ((row >> 1) & 7) : ((row >> 2) & 3);
@@ -177,21 +180,28 @@ __device__ __forceinline__ void run_epilogue(const GemmArgs& a, ACC (&acc)[C::RN
         }
       }
     } else {
-      // bias (and int8 weight scale) of this lane's output columns, hoisted out of the row loop
-      float bv[C::RN][4][4];
-      float swv[C::RN][4][4];
-#pragma unroll
-      for (int i = 0; i < C::RN; ++i)
+      // bias (and int8 weight scale) of this lane's output columns, hoisted out of
+      // the row loop for narrow wave tiles (wide ones reload them: registers)
+      constexpr bool kHoist = C::RN <= 2;
+      constexpr int HN = kHoist ? C::RN : 1;
+      float bv[HN][4][4];
+      float swv[HN][4][4];
+      auto load_cols = [&](int i, int hi_, float (&b4)[4][4], float (&w4)[4][4]) {
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
-          const int n = n0 + wn * C::WTN + i * 32 + 8 * g + 4 * hi;
-          if (a.bias) unpack4(*reinterpret_cast<const uint2*>(a.bias + n), bv[i][g]);
-          else bv[i][g][0] = bv[i][g][1] = bv[i][g][2] = bv[i][g][3] = 0.f;
+          const int n = n0 + wn * C::WTN + i * 32 + 8 * g + 4 * hi_;
+          if (a.bias) unpack4(*reinterpret_cast<const uint2*>(a.bias + n), b4[g]);
+          else b4[g][0] = b4[g][1] = b4[g][2] = b4[g][3] = 0.f;
           if constexpr (EPI == EPI_DQ) {
-            const float4 w4 = *reinterpret_cast<const float4*>(a.sw + n);
-            swv[i][g][0] = w4.x; swv[i][g][1] = w4.y; swv[i][g][2] = w4.z; swv[i][g][3] = w4.w;
+            const float4 q4 = *reinterpret_cast<const float4*>(a.sw + n);
+            w4[g][0] = q4.x; w4[g][1] = q4.y; w4[g][2] = q4.z; w4[g][3] = q4.w;
           }
         }
+      };
+      if constexpr (kHoist) {
+#pragma unroll
+        for (int i = 0; i < C::RN; ++i) load_cols(i, hi, bv[i], swv[i]);
+      }
       const bool full = m0 + wm * C::WTM + C::WTM <= M;  // wave-uniform: no row past M
 #pragma unroll
       for (int k = 0; k < C::RM; ++k) {
@@ -205,6 +215,9 @@ __device__ __forceinline__ void run_epilogue(const GemmArgs& a, ACC (&acc)[C::RN
 #pragma unroll
         for (int i = 0; i < C::RN; ++i) {
           const int nb = n0 + wn * C::WTN + i * 32 + 4 * hi;
+          float (&bvi)[4][4] = bv[kHoist ? i : 0];
+          float (&swi)[4][4] = swv[kHoist ? i : 0];
+          if constexpr (!kHoist) load_cols(i, hi, bvi, swi);
 #pragma unroll
           for (int g = 0; g < 4; ++g) {
             const int n = nb + 8 * g;
@@ -217,10 +230,10 @@ __device__ __forceinline__ void run_epilogue(const GemmArgs& a, ACC (&acc)[C::RN
               // ((acc.f32 * s_x) * s_w) + bias, each op rounded to float32 (int8_dit.py:60-62)
 #pragma unroll
               for (int t = 0; t < 4; ++t)
-                y[t] = add_rn(mul_rn(mul_rn((float)acc[i][k][4 * g + t], sxm), swv[i][g][t]), bv[i][g][t]);
+                y[t] = add_rn(mul_rn(mul_rn((float)acc[i][k][4 * g + t], sxm), swi[g][t]), bvi[g][t]);
             } else {
 #pragma unroll
-              for (int t = 0; t < 4; ++t) y[t] = acc[i][k][4 * g + t] + bv[i][g][t];
+              for (int t = 0; t < 4; ++t) y[t] = acc[i][k][4 * g + t] + bvi[g][t];
             }
             if constexpr (EPI == EPI_F32) {
               *reinterpret_cast<float4*>(a.Cf + (long)m * a.ldc + n) = make_float4(y[0], y[1], y[2], y[3]);
@@ -288,40 +301,63 @@ gemm_mfma_kernel(GemmArgs a) {
   const int per_xcd = gridDim.x / nxcd;
   const int chunk = (total + nxcd - 1) / nxcd;
   auto tile_at = [&](int jt) { const int t = xcd * chunk + jt; return (jt < chunk && t < total) ? t : -1; };
+  // Grouped order: the per_xcd tiles an XCD runs at once cover GM row blocks x
+  // per_xcd/GM column blocks (row block fastest), so each A row block and W
+  // column block is fetched into that XCD's L2 once per round, not per tile.
+  const int gn = tiles_n < 8 ? tiles_n : 8;
+  const int GM = per_xcd / gn > 1 ? per_xcd / gn : 1;
+  auto tile_mn = [&](int t, int& m0, int& n0) {
+    const int gsz = GM * tiles_n;
+    const int g = t / gsz, w = t - g * gsz;
+    const int gm0 = g * GM;
+    const int rows = tiles_m - gm0 < GM ? tiles_m - gm0 : GM;
+    m0 = (gm0 + w % rows) * BM;
+    n0 = (w / rows) * BN;
+  };
 
   // DMA: lane L of wave w, load j -> tile row j*RPR + w*ROWS_PER_DMA + L/CH, slot L%CH,
-  // i.e. source chunk (L%CH) ^ swz(row)
+  // i.e. source chunk (L%CH) ^ swz(row); swz(row) is the same for every j (RPR % 16 == 0).
+  // Buffer loads with a per-tile resource: rows at or past M fall outside the
+  // resource's range and arrive as zeros, so no row clamping; per lane only one
+  // 32-bit byte offset per operand stays live.
+  static_assert(C::RPR % 16 == 0, "swizzle must not depend on the DMA round");
   const int dma_row = wave * C::ROWS_PER_DMA + lane / CH;
-  int a_off[C::AJ], b_off[C::BJ];
+  const uint32_t dma_col = (uint32_t)(((lane % CH) ^ swz<CH>(dma_row)) << 3);
+  const uint32_t va = ((uint32_t)dma_row * (uint32_t)a.lda + dma_col) * 2u;
+  const uint32_t vb = ((uint32_t)dma_row * (uint32_t)a.ldb + dma_col) * 2u;
+  const uint32_t a_round = (uint32_t)C::RPR * (uint32_t)a.lda * 2u;
+  const uint32_t b_round = (uint32_t)C::RPR * (uint32_t)a.ldb * 2u;
+  __amdgpu_buffer_rsrc_t ra, rb;
   auto set_offsets = [&](int tile) {
-    const int m0 = (tile / tiles_n) * BM, n0 = (tile % tiles_n) * BN;
-#pragma unroll
-    for (int j = 0; j < C::AJ; ++j) {
-      const int r = j * C::RPR + dma_row;
-      int gm = m0 + r;
-      gm = gm < M ? gm : M - 1;
-      a_off[j] = gm * (int)a.lda + (((lane % CH) ^ swz<CH>(r)) << 3);
-    }
-#pragma unroll
-    for (int j = 0; j < C::BJ; ++j) {
-      const int r = j * C::RPR + dma_row;
-      b_off[j] = (n0 + r) * (int)a.ldb + (((lane % CH) ^ swz<CH>(r)) << 3);
-    }
+    int m0, n0;
+    tile_mn(tile, m0, n0);
+    ra = __builtin_amdgcn_make_buffer_rsrc((void*)(a.A + (long)m0 * a.lda), (short)0,
+                                           (int)((uint32_t)(M - m0) * (uint32_t)a.lda * 2u), kBufferFlags);
+    rb = __builtin_amdgcn_make_buffer_rsrc((void*)(a.B + (long)n0 * a.ldb), (short)0,
+                                           (int)((uint32_t)BN * (uint32_t)a.ldb * 2u), kBufferFlags);
   };
   auto dma = [&](auto stc, int kstep) {
     uint16_t* la = stA(stc);
     uint16_t* lb = stB(stc);
-    const int koff = kstep * BK;
+    const int koff = kstep * BK * 2;
+    // the per-round offsets are recomputed here (the empty asm hides them from
+    // loop-invariant hoisting, which would pin AJ + BJ registers for the whole kernel)
+    uint32_t vo = va;
 #pragma unroll
-    for (int j = 0; j < C::AJ; ++j)
-      __builtin_amdgcn_global_load_lds(DFH_GPTR(a.A + a_off[j] + koff),
-                                       DFH_LPTR(la + (j * C::RPR + wave * C::ROWS_PER_DMA) * BK), 16, 0,
-                                       0);
+    for (int j = 0; j < C::AJ; ++j) {
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, DFH_LPTR(la + (j * C::RPR + wave * C::ROWS_PER_DMA) * BK), 16,
+                                               vo, koff, 0, 0);
+      vo += a_round;
+      asm volatile("" : "+v"(vo));
+    }
+    vo = vb;
 #pragma unroll
-    for (int j = 0; j < C::BJ; ++j)
-      __builtin_amdgcn_global_load_lds(DFH_GPTR(a.B + b_off[j] + koff),
-                                       DFH_LPTR(lb + (j * C::RPR + wave * C::ROWS_PER_DMA) * BK), 16, 0,
-                                       0);
+    for (int j = 0; j < C::BJ; ++j) {
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, DFH_LPTR(lb + (j * C::RPR + wave * C::ROWS_PER_DMA) * BK), 16,
+                                               vo, koff, 0, 0);
+      vo += b_round;
+      asm volatile("" : "+v"(vo));
+    }
   };
 
   const int fa_row = wm * C::WTM + l32;
@@ -372,7 +408,8 @@ gemm_mfma_kernel(GemmArgs a) {
     prologue();
   }
   while (tile >= 0) {
-    const int m0 = (tile / tiles_n) * BM, n0 = (tile % tiles_n) * BN;
+    int m0, n0;
+    tile_mn(tile, m0, n0);
 #pragma unroll
     for (int i = 0; i < C::RN; ++i)
 #pragma unroll
