@@ -148,7 +148,9 @@ int tile_for(long M, int N, int K, GemmRole role) {
   if (role == kRoleQKV) return 2;
   if (role == kRoleWide) return N % 256 == 0 ? 0 : -1;
   if (K >= 4096 && N % 256 == 0) return 0;
-  return (N % 256 == 0 && K % 32 == 0) ? 5 : -1;
+  // narrow outputs (N = hidden) at K = hidden: 128x128 tiles, two workgroups per
+  // CU; 256-wide tiles (N/256 column blocks) leave up to a third of the last round idle
+  return (N % 128 == 0 && K % 64 == 0) ? 2 : -1;
 }
 
 GemmArgs linear_args(const uint16_t* A, long lda, const uint16_t* W, const uint16_t* b, uint16_t* C,

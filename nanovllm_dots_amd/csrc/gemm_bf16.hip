@@ -58,6 +58,8 @@ struct Cfg {
 // (row, slot) -> (row*CH + slot) % 16 all distinct.
 // buffer resource word 3 for gfx9-family raw (stride 0) buffers: 32-bit data format
 constexpr int kBufferFlags = 0x00020000;
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 template <int CH>
 __device__ __forceinline__ int swz(int row) {
@@ -88,97 +90,219 @@ struct OpI8 {
 
 
 
+// Epilogues whose bf16 output goes through LDS: each wave writes one 32-row
+// block of its tile into a private region of the stage the main loop is not
+// filling, then stores it back as whole rows, 16 B per lane (8 full 128-B rows
+// per store instruction instead of 32 partial rows). Needs NW * 32 * WTN bf16
+// of free stage: half the waves in the A buffer, half in the B buffer.
+template <class C, int EPI>
+struct Staged {
+  static constexpr bool kEpi = EPI == EPI_BIAS || EPI == EPI_GELU;
+  static constexpr int kSmall = C::BM < C::BN ? C::BM : C::BN;
+  static constexpr bool value = kEpi && (C::NW / 2) * 32 * C::WTN <= kSmall * C::BK && C::NW % 2 == 0;
+  static constexpr int CPR = C::WTN / 8;   // 16-B chunks per staged row
+  static constexpr int RPI = 64 / CPR;     // rows per wave-wide 16-B access
+  static constexpr int kStores = C::RM * (32 / RPI);
+};
+
+// staged element offset: row r (0..31) of the block, 16-B chunk c, slot c ^ ((r >> 1) & 7)
+template <int CPR>
+__device__ __forceinline__ int stage_off(int r, int c) {
+  return r * CPR * 8 + ((c ^ ((r >> 1) & (CPR - 1))) << 3);
+}
+
+// Column operands of a staged epilogue (bias, int8 weight scales) and the row
+// scales of W8A8, loaded BEFORE the next tile's prologue DMA: vmcnt completes
+// in issue order, so a later load would make its first use wait for that DMA.
+template <class C, int EPI>
+struct StagedOperands {
+  float b[C::RN][4][4];
+  float w[EPI == EPI_DQ ? C::RN : 1][4][4];
+  float sx[EPI == EPI_DQ ? C::RM : 1];
+};
+
+template <class C, int EPI>
+__device__ __forceinline__ void staged_preload(const GemmArgs& a, StagedOperands<C, EPI>& op, int m0, int n0,
+                                               int M, int wm, int wn, int l32, int hi) {
+  // one uniform branch around all loads, so they issue back to back and are waited for once
+  uint2 braw[C::RN][4];
+  if (a.bias) {
+#pragma unroll
+    for (int i = 0; i < C::RN; ++i)
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+        braw[i][g] = *reinterpret_cast<const uint2*>(a.bias + n0 + wn * C::WTN + i * 32 + 8 * g + 4 * hi);
+  } else {
+#pragma unroll
+    for (int i = 0; i < C::RN; ++i)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) braw[i][g] = make_uint2(0u, 0u);
+  }
+#pragma unroll
+  for (int i = 0; i < C::RN; ++i)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int n = n0 + wn * C::WTN + i * 32 + 8 * g + 4 * hi;
+      unpack4(braw[i][g], op.b[i][g]);
+      if constexpr (EPI == EPI_DQ) {
+        const float4 w4 = *reinterpret_cast<const float4*>(a.sw + n);
+        op.w[i][g][0] = w4.x; op.w[i][g][1] = w4.y; op.w[i][g][2] = w4.z; op.w[i][g][3] = w4.w;
+      }
+    }
+  if constexpr (EPI == EPI_DQ) {
+#pragma unroll
+    for (int k = 0; k < C::RM; ++k) {
+      const int m = m0 + wm * C::WTM + k * 32 + l32;
+      op.sx[k] = a.sx[m < M ? m : M - 1];
+    }
+  }
+}
+
+template <class C, int EPI, class ACC>
+__device__ __forceinline__ void staged_epilogue(const GemmArgs& a, ACC (&acc)[C::RN][C::RM],
+                                                const StagedOperands<C, EPI>& op, int m0, int n0, int M,
+                                                int wm, int wn, int lane, int l32, int hi, uint16_t* region) {
+  using S = Staged<C, EPI>;
+  constexpr int CPR = S::CPR, RPI = S::RPI;
+  const __amdgpu_buffer_rsrc_t rc = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(a.C + (long)m0 * a.ldc), (short)0, (int)((uint32_t)(M - m0) * (uint32_t)a.ldc * 2u), kBufferFlags);
+  const int ncol0 = n0 + wn * C::WTN;
+#pragma unroll
+  for (int k = 0; k < C::RM; ++k) {
+    // MFMA layout -> LDS: lane (l32, hi) holds row l32, columns i*32 + 8g + 4hi + [0, 4)
+#pragma unroll
+    for (int i = 0; i < C::RN; ++i)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        float y[4];
+        if constexpr (EPI == EPI_DQ) {
+          // ((acc.f32 * s_x) * s_w) + bias, each op rounded to float32 (int8_dit.py:60-62)
+#pragma unroll
+          for (int t = 0; t < 4; ++t)
+            y[t] = add_rn(mul_rn(mul_rn((float)acc[i][k][4 * g + t], op.sx[k]), op.w[i][g][t]), op.b[i][g][t]);
+        } else {
+#pragma unroll
+          for (int t = 0; t < 4; ++t) y[t] = acc[i][k][4 * g + t] + op.b[i][g][t];
+        }
+        if constexpr (EPI == EPI_GELU) {
+#pragma unroll
+          for (int t = 0; t < 4; ++t) y[t] = gelu_tanh_f(rbf(y[t]));
+        }
+        *reinterpret_cast<uint2*>(region + stage_off<CPR>(l32, 4 * i + g) + 4 * hi) = pack4(y[0], y[1], y[2], y[3]);
+      }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    // LDS -> rows: lane reads 16 B of row j*RPI + lane/CPR and stores it
+#pragma unroll
+    for (int j = 0; j < 32 / RPI; ++j) {
+      const int r = j * RPI + lane / CPR, c = lane % CPR;
+      const uint4 v = *reinterpret_cast<const uint4*>(region + stage_off<CPR>(r, c));
+      const int rt = wm * C::WTM + k * 32 + r;  // row within the tile
+      const int n = ncol0 + c * 8;
+      const u32x4 o = {v.x, v.y, v.z, v.w};
+      __builtin_amdgcn_raw_buffer_store_b128(o, rc, ((uint32_t)rt * (uint32_t)a.ldc + (uint32_t)n) * 2u, 0, 0);
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // reads done before the next block overwrites
+  }
+}
+
+// q / k: bias, optional per-head LayerNorm / RMSNorm over 64, RoPE on the
+// column pairs (d, d+32) that a lane holds in blocks (i, i+1); v: transposed
+// into V^T[column][vt_col[row]].
+template <class C, class ACC>
+__device__ __forceinline__ void qkv_epilogue(const GemmArgs& a, ACC (&acc)[C::RN][C::RM], int m0, int n0,
+                                             int M, int wm, int wn, int l32, int hi) {
+  const int H = a.hidden;
+  const int region = n0 / H;  // 0 q, 1 k, 2 v (BN divides H)
+#pragma unroll
+  for (int k = 0; k < C::RM; ++k) {
+    const int m = m0 + wm * C::WTM + k * 32 + l32;
+    const bool valid = m < M;
+    const int mm = valid ? m : M - 1;
+    if (region == 2) {
+      const int col = a.vt_col[mm];
+#pragma unroll
+      for (int i = 0; i < C::RN; ++i) {
+        const int nb = n0 + wn * C::WTN + i * 32 - 2 * H;
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int n = nb + 8 * (v >> 2) + 4 * hi + (v & 3);
+          float y = acc[i][k][v] + (a.bias ? bf2f(a.bias[n + 2 * H]) : 0.f);
+          if (valid) a.vt[(long)n * a.ld_vt + col] = f2bf(y);
+        }
+      }
+      continue;
+    }
+    const uint16_t* nw = region == 0 ? a.qn_w : a.kn_w;
+    const uint16_t* nbias = region == 0 ? a.qn_b : a.kn_b;
+    const int pos = a.row_pos[mm];
+    // heads are pairs of 32-column blocks (i, i+1): d in [0,32) and [32,64)
+#pragma unroll
+    for (int i = 0; i < C::RN; i += 2) {
+      const int nb = n0 + wn * C::WTN + i * 32;  // head start column (within q|k|v)
+      float x0[16], x1[16];
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int d = 8 * (v >> 2) + 4 * hi + (v & 3);
+        float b0 = a.bias ? bf2f(a.bias[nb + d]) : 0.f;
+        float b1 = a.bias ? bf2f(a.bias[nb + 32 + d]) : 0.f;
+        x0[v] = rbf(acc[i][k][v] + b0);
+        x1[v] = rbf(acc[i + 1][k][v] + b1);
+      }
+      if (a.qk_norm) {
+        float s = 0.f, s2 = 0.f;
+#pragma unroll
+        for (int v = 0; v < 16; ++v) { s += x0[v] + x1[v]; }
+        s += __shfl_xor(s, 32, 64);
+        float mean = a.qk_norm == 1 ? s * (1.0f / 64.0f) : 0.f;
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          float d0 = x0[v] - mean, d1 = x1[v] - mean;
+          s2 += d0 * d0 + d1 * d1;
+        }
+        s2 += __shfl_xor(s2, 32, 64);
+        const float eps = a.qk_norm == 1 ? 1e-5f : 1.1920928955078125e-07f;
+        const float rstd = rsqrtf(s2 * (1.0f / 64.0f) + eps);
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int d = 8 * (v >> 2) + 4 * hi + (v & 3);
+          float w0 = bf2f(nw[d]), w1 = bf2f(nw[d + 32]);
+          float c0 = (a.qk_norm == 1) ? bf2f(nbias[d]) : 0.f;
+          float c1 = (a.qk_norm == 1) ? bf2f(nbias[d + 32]) : 0.f;
+          x0[v] = (x0[v] - mean) * rstd * w0 + c0;
+          x1[v] = (x1[v] - mean) * rstd * w1 + c1;
+        }
+      }
+      if (a.rope_cos) {
+        const float* cs = a.rope_cos + (long)pos * 32;
+        const float* sn = a.rope_sin + (long)pos * 32;
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int d = 8 * (v >> 2) + 4 * hi + (v & 3);
+          const float c = cs[d], s = sn[d];
+          const float r0 = add_rn(mul_rn(x0[v], c), mul_rn(-x1[v], s));
+          const float r1 = add_rn(mul_rn(x1[v], c), mul_rn(x0[v], s));
+          x0[v] = r0;
+          x1[v] = r1;
+        }
+      }
+      if (valid) {
+        uint16_t* cp = a.C + (long)(a.c_rows ? a.c_rows[m] : m) * a.ldc + nb;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int d = 8 * g + 4 * hi;
+          *reinterpret_cast<uint2*>(cp + d) = pack4(x0[4 * g], x0[4 * g + 1], x0[4 * g + 2], x0[4 * g + 3]);
+          *reinterpret_cast<uint2*>(cp + 32 + d) = pack4(x1[4 * g], x1[4 * g + 1], x1[4 * g + 2], x1[4 * g + 3]);
+        }
+      }
+    }
+  }
+}
+
 template <class C, int EPI, class ACC>
 __device__ __forceinline__ void run_epilogue(const GemmArgs& a, ACC (&acc)[C::RN][C::RM], int m0,
                                              int n0, int M, int wm, int wn, int l32, int hi) {
     if constexpr (EPI == EPI_QKV) {
-      const int H = a.hidden;
-      const int region = n0 / H;  // 0 q, 1 k, 2 v (BN divides H)
-#pragma unroll
-      for (int k = 0; k < C::RM; ++k) {
-        const int m = m0 + wm * C::WTM + k * 32 + l32;
-        const bool valid = m < M;
-        const int mm = valid ? m : M - 1;
-        if (region == 2) {
-          const int col = a.vt_col[mm];
-#pragma unroll
-          for (int i = 0; i < C::RN; ++i) {
-            const int nb = n0 + wn * C::WTN + i * 32 - 2 * H;
-#pragma unroll
-            for (int v = 0; v < 16; ++v) {
-              const int n = nb + 8 * (v >> 2) + 4 * hi + (v & 3);
-              float y = acc[i][k][v] + (a.bias ? bf2f(a.bias[n + 2 * H]) : 0.f);
-              if (valid) a.vt[(long)n * a.ld_vt + col] = f2bf(y);
-            }
-          }
-          continue;
-        }
-        const uint16_t* nw = region == 0 ? a.qn_w : a.kn_w;
-        const uint16_t* nbias = region == 0 ? a.qn_b : a.kn_b;
-        const int pos = a.row_pos[mm];
-        // heads are pairs of 32-column blocks (i, i+1): d in [0,32) and [32,64)
-#pragma unroll
-        for (int i = 0; i < C::RN; i += 2) {
-          const int nb = n0 + wn * C::WTN + i * 32;  // head start column (within q|k|v)
-          float x0[16], x1[16];
-#pragma unroll
-          for (int v = 0; v < 16; ++v) {
-            const int d = 8 * (v >> 2) + 4 * hi + (v & 3);
-            float b0 = a.bias ? bf2f(a.bias[nb + d]) : 0.f;
-            float b1 = a.bias ? bf2f(a.bias[nb + 32 + d]) : 0.f;
-            x0[v] = rbf(acc[i][k][v] + b0);
-            x1[v] = rbf(acc[i + 1][k][v] + b1);
-          }
-          if (a.qk_norm) {
-            float s = 0.f, s2 = 0.f;
-#pragma unroll
-            for (int v = 0; v < 16; ++v) { s += x0[v] + x1[v]; }
-            s += __shfl_xor(s, 32, 64);
-            float mean = a.qk_norm == 1 ? s * (1.0f / 64.0f) : 0.f;
-#pragma unroll
-            for (int v = 0; v < 16; ++v) {
-              float d0 = x0[v] - mean, d1 = x1[v] - mean;
-              s2 += d0 * d0 + d1 * d1;
-            }
-            s2 += __shfl_xor(s2, 32, 64);
-            const float eps = a.qk_norm == 1 ? 1e-5f : 1.1920928955078125e-07f;
-            const float rstd = rsqrtf(s2 * (1.0f / 64.0f) + eps);
-#pragma unroll
-            for (int v = 0; v < 16; ++v) {
-              const int d = 8 * (v >> 2) + 4 * hi + (v & 3);
-              float w0 = bf2f(nw[d]), w1 = bf2f(nw[d + 32]);
-              float c0 = (a.qk_norm == 1) ? bf2f(nbias[d]) : 0.f;
-              float c1 = (a.qk_norm == 1) ? bf2f(nbias[d + 32]) : 0.f;
-              x0[v] = (x0[v] - mean) * rstd * w0 + c0;
-              x1[v] = (x1[v] - mean) * rstd * w1 + c1;
-            }
-          }
-          if (a.rope_cos) {
-            const float* cs = a.rope_cos + (long)pos * 32;
-            const float* sn = a.rope_sin + (long)pos * 32;
-#pragma unroll
-            for (int v = 0; v < 16; ++v) {
-              const int d = 8 * (v >> 2) + 4 * hi + (v & 3);
-              const float c = cs[d], s = sn[d];
-              const float r0 = add_rn(mul_rn(x0[v], c), mul_rn(-x1[v], s));
-              const float r1 = add_rn(mul_rn(x1[v], c), mul_rn(x0[v], s));
-              x0[v] = r0;
-              x1[v] = r1;
-            }
-          }
-          if (valid) {
-            uint16_t* cp = a.C + (long)(a.c_rows ? a.c_rows[m] : m) * a.ldc + nb;
-#pragma unroll
-            for (int g = 0; g < 4; ++g) {
-              const int d = 8 * g + 4 * hi;
-              *reinterpret_cast<uint2*>(cp + d) =
-                  pack4(x0[4 * g], x0[4 * g + 1], x0[4 * g + 2], x0[4 * g + 3]);
-              *reinterpret_cast<uint2*>(cp + 32 + d) =
-                  pack4(x1[4 * g], x1[4 * g + 1], x1[4 * g + 2], x1[4 * g + 3]);
-            }
-          }
-        }
-      }
+      qkv_epilogue<C>(a, acc, m0, n0, M, wm, wn, l32, hi);
     } else {
       // bias (and int8 weight scale) of this lane's output columns, hoisted out of
       // the row loop for narrow wave tiles (wide ones reload them: registers)
@@ -187,11 +311,19 @@ __device__ __forceinline__ void run_epilogue(const GemmArgs& a, ACC (&acc)[C::RN
       float bv[HN][4][4];
       float swv[HN][4][4];
       auto load_cols = [&](int i, int hi_, float (&b4)[4][4], float (&w4)[4][4]) {
+        uint2 braw[4];
+        if (a.bias) {
+#pragma unroll
+          for (int g = 0; g < 4; ++g)
+            braw[g] = *reinterpret_cast<const uint2*>(a.bias + n0 + wn * C::WTN + i * 32 + 8 * g + 4 * hi_);
+        } else {
+#pragma unroll
+          for (int g = 0; g < 4; ++g) braw[g] = make_uint2(0u, 0u);
+        }
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
           const int n = n0 + wn * C::WTN + i * 32 + 8 * g + 4 * hi_;
-          if (a.bias) unpack4(*reinterpret_cast<const uint2*>(a.bias + n), b4[g]);
-          else b4[g][0] = b4[g][1] = b4[g][2] = b4[g][3] = 0.f;
+          unpack4(braw[g], b4[g]);
           if constexpr (EPI == EPI_DQ) {
             const float4 q4 = *reinterpret_cast<const float4*>(a.sw + n);
             w4[g][0] = q4.x; w4[g][1] = q4.y; w4[g][2] = q4.z; w4[g][3] = q4.w;
@@ -202,16 +334,27 @@ __device__ __forceinline__ void run_epilogue(const GemmArgs& a, ACC (&acc)[C::RN
 #pragma unroll
         for (int i = 0; i < C::RN; ++i) load_cols(i, hi, bv[i], swv[i]);
       }
-      const bool full = m0 + wm * C::WTM + C::WTM <= M;  // wave-uniform: no row past M
+      // Rows [m0, M) of the output through a range-limited buffer resource:
+      // stores to rows at or past M are dropped by the hardware, so the
+      // epilogue has no row branches and always issues RN*RM*4 stores (the
+      // tile-start wait of the main loop counts on that). Table lookups and
+      // residual reads use the row clamped to M - 1.
+      constexpr int ESZ = (EPI == EPI_F32 || EPI == EPI_I32) ? 4 : 2;
+      void* cbase = EPI == EPI_F32 ? (void*)(a.Cf + (long)m0 * a.ldc)
+                  : EPI == EPI_I32 ? (void*)(a.Ci + (long)m0 * a.ldc)
+                                   : (void*)(a.C + (long)m0 * a.ldc);
+      const __amdgpu_buffer_rsrc_t rc = __builtin_amdgcn_make_buffer_rsrc(
+          cbase, (short)0, (int)((uint32_t)(M - m0) * (uint32_t)a.ldc * (uint32_t)ESZ), kBufferFlags);
 #pragma unroll
       for (int k = 0; k < C::RM; ++k) {
-        const int m = m0 + wm * C::WTM + k * 32 + l32;
-        if (!full && m >= M) continue;
-        uint16_t* crow = a.C + (long)m * a.ldc;
+        const int r = wm * C::WTM + k * 32 + l32;  // row within the tile
+        const int mm = m0 + r < M ? m0 + r : M - 1;
+        const uint32_t rowoff = (uint32_t)r * (uint32_t)a.ldc;
+        const uint16_t* xrow = a.C + (long)mm * a.ldc;
         const uint16_t* grow = nullptr;
-        if constexpr (EPI == EPI_GATE_RES) grow = a.gate + (long)a.row_req[m] * a.ld_gate;
+        if constexpr (EPI == EPI_GATE_RES) grow = a.gate + (long)a.row_req[mm] * a.ld_gate;
         float sxm = 0.f;
-        if constexpr (EPI == EPI_DQ) sxm = a.sx[m];
+        if constexpr (EPI == EPI_DQ) sxm = a.sx[mm];
 #pragma unroll
         for (int i = 0; i < C::RN; ++i) {
           const int nb = n0 + wn * C::WTN + i * 32 + 4 * hi;
@@ -221,10 +364,12 @@ __device__ __forceinline__ void run_epilogue(const GemmArgs& a, ACC (&acc)[C::RN
 #pragma unroll
           for (int g = 0; g < 4; ++g) {
             const int n = nb + 8 * g;
+            const uint32_t off = (rowoff + (uint32_t)n) * (uint32_t)ESZ;
             float y[4];
             if constexpr (EPI == EPI_I32) {
-              *reinterpret_cast<int4*>(a.Ci + (long)m * a.ldc + n) =
-                  make_int4(acc[i][k][4 * g], acc[i][k][4 * g + 1], acc[i][k][4 * g + 2], acc[i][k][4 * g + 3]);
+              const u32x4 v = {(uint32_t)acc[i][k][4 * g], (uint32_t)acc[i][k][4 * g + 1],
+                               (uint32_t)acc[i][k][4 * g + 2], (uint32_t)acc[i][k][4 * g + 3]};
+              __builtin_amdgcn_raw_buffer_store_b128(v, rc, off, 0, 0);
               continue;
             } else if constexpr (EPI == EPI_DQ) {
               // ((acc.f32 * s_x) * s_w) + bias, each op rounded to float32 (int8_dit.py:60-62)
@@ -236,7 +381,9 @@ __device__ __forceinline__ void run_epilogue(const GemmArgs& a, ACC (&acc)[C::RN
               for (int t = 0; t < 4; ++t) y[t] = acc[i][k][4 * g + t] + bvi[g][t];
             }
             if constexpr (EPI == EPI_F32) {
-              *reinterpret_cast<float4*>(a.Cf + (long)m * a.ldc + n) = make_float4(y[0], y[1], y[2], y[3]);
+              const u32x4 v = {__float_as_uint(y[0]), __float_as_uint(y[1]), __float_as_uint(y[2]),
+                               __float_as_uint(y[3])};
+              __builtin_amdgcn_raw_buffer_store_b128(v, rc, off, 0, 0);
               continue;
             } else if constexpr (EPI == EPI_GELU) {
 #pragma unroll
@@ -244,12 +391,14 @@ __device__ __forceinline__ void run_epilogue(const GemmArgs& a, ACC (&acc)[C::RN
             } else if constexpr (EPI == EPI_GATE_RES) {
               float gt[4], xr[4];
               unpack4(*reinterpret_cast<const uint2*>(grow + n), gt);
-              unpack4(*reinterpret_cast<const uint2*>(crow + n), xr);
+              unpack4(*reinterpret_cast<const uint2*>(xrow + n), xr);
 #pragma unroll
               for (int t = 0; t < 4; ++t) y[t] = xr[t] + rbf(gt[t] * rbf(y[t]));
             }
             // EPI_BIAS: one rounding, inside the pack
-            *reinterpret_cast<uint2*>(crow + n) = pack4(y[0], y[1], y[2], y[3]);
+            const uint2 pk = pack4(y[0], y[1], y[2], y[3]);
+            const u32x2 v = {pk.x, pk.y};
+            __builtin_amdgcn_raw_buffer_store_b64(v, rc, off, 0, 0);
           }
         }
       }
@@ -385,12 +534,33 @@ gemm_mfma_kernel(GemmArgs a) {
   };
 
   const int KT = K / BK;
+  // Vector-memory ops decrement vmcnt in issue order. The epilogue issues
+  // exactly kEpiStores stores after the next tile's prologue DMA, so that
+  // tile's first step waits for vmcnt <= kEpiStores (+ the later prologue
+  // stages) and leaves the stores in flight. The QKV epilogue (data-dependent
+  // store count) waits for zero.
+  constexpr int kEpiStores = (EPI == EPI_QKV) ? -1 : Staged<C, EPI>::value ? Staged<C, EPI>::kStores
+                                                                          : C::RN * C::RM * 4;
+  constexpr int kStartWait = (ST >= 2 ? (ST - 2) * C::LPS : 0) + (kEpiStores > 0 ? kEpiStores : 0);
+  static_assert(kStartWait < 64, "vmcnt range");
   // one pipelined K step: k = step index, stage s = k % ST (compile-time)
   auto step = [&](auto stc, int k) {
     constexpr int s = decltype(stc)::value;
     if (k >= KT) return;  // uniform
-    if (k == 0 || k + ST - 2 >= KT) wait_vm_lgkm0<0>();   // tile start / pipeline drain: exact
-    else wait_vm_lgkm0<(ST >= 2 ? (ST - 2) * C::LPS : 0)>();
+    if (k == 0) {
+      if constexpr (kEpiStores >= 0 && ST == 2) {
+        wait_vm_lgkm0<kStartWait>();
+      } else if constexpr (kEpiStores >= 0) {
+        if (KT >= ST - 1) wait_vm_lgkm0<(kEpiStores >= 0 ? kStartWait : 0)>();
+        else wait_vm_lgkm0<0>();
+      } else {
+        wait_vm_lgkm0<0>();
+      }
+    } else if (k + ST - 2 >= KT) {
+      wait_vm_lgkm0<0>();   // pipeline drain: exact
+    } else {
+      wait_vm_lgkm0<(ST >= 2 ? (ST - 2) * C::LPS : 0)>();
+    }
     __builtin_amdgcn_s_barrier();
     if (k + ST - 1 < KT) dma(std::integral_constant<int, (s + ST - 1) % ST>{}, k + ST - 1);
     compute(stc);
@@ -406,6 +576,7 @@ gemm_mfma_kernel(GemmArgs a) {
   if (tile >= 0) {
     set_offsets(tile);
     prologue();
+    wait_vm_lgkm0<0>();  // the first tile has no epilogue stores in flight
   }
   while (tile >= 0) {
     int m0, n0;
@@ -425,6 +596,8 @@ gemm_mfma_kernel(GemmArgs a) {
     // every wave is done with every stage before it is refilled
     wait_vm_lgkm0<0>();
     __builtin_amdgcn_s_barrier();
+    StagedOperands<C, EPI> sop;
+    if constexpr (Staged<C, EPI>::value) staged_preload<C, EPI>(a, sop, m0, n0, M, wm, wn, l32, hi);
     // start the next tile's first K steps under this tile's epilogue
     jt += per_xcd;
     const int next = tile_at(jt);
@@ -432,7 +605,16 @@ gemm_mfma_kernel(GemmArgs a) {
       set_offsets(next);
       prologue();
     }
-    run_epilogue<C, EPI>(a, acc, m0, n0, M, wm, wn, l32, hi);
+    if constexpr (Staged<C, EPI>::value) {
+      // the stage the prologue does not fill (ST - 1); waves split over its A and B buffers
+      constexpr int fs = ST - 1;
+      uint16_t* region = (wave < C::NW / 2 ? stA(std::integral_constant<int, fs>{})
+                                           : stB(std::integral_constant<int, fs>{})) +
+                         (wave % (C::NW / 2)) * 32 * C::WTN;
+      staged_epilogue<C, EPI>(a, acc, sop, m0, n0, M, wm, wn, lane, l32, hi, region);
+    } else {
+      run_epilogue<C, EPI>(a, acc, m0, n0, M, wm, wn, l32, hi);
+    }
     tile = next;
   }
 }
