@@ -124,12 +124,23 @@ int dfh_input_status(DfhHandle* h, int* flags, void* stream);
  * classes: 0 qkv gemm, 1 o_proj gemm, 2 fc1 gemm, 3 fc2 gemm, 4 attention,
  * 5 ln_modulate, 6 other. */
 int dfh_profile_enable(DfhHandle* h, int enable);
+/* K-split of each GEMM's last, partial round of tiles (default on): leftover
+ * tiles are cut along K over the idle workgroups, with a second kernel that
+ * adds the partial sums. Off: every tile runs whole. No reference counterpart
+ * (a scheduling choice of this library; results agree to float32 summation order). */
+int dfh_set_ksplit(DfhHandle* h, int enable);
 int dfh_profile_read(DfhHandle* h, double* ms_per_class, long* launches_per_class, int n_classes);
 
 /* Standalone bf16 GEMM: C[M,N] = A[M,K] B[N,K]^T + bias (bias may be NULL).
  * epilogue: 0 bf16 out, 1 GELU(tanh) bf16 out, 4 float32 out. */
 int dfh_gemm_bf16(const void* A, long lda, const void* B, long ldb, void* C, long ldc,
                   const void* bias, int M, int N, int K, int epilogue, int tile, void* stream);
+/* dfh_gemm_bf16 with a device workspace (ws, ws_bytes) for the K-split of the
+ * last partial round of tiles (see dfh_set_ksplit); too small or NULL: no split.
+ * ws_bytes >= 4 * 65536 * (number of CUs) always suffices. */
+int dfh_gemm_bf16_ws(const void* A, long lda, const void* B, long ldb, void* C, long ldc,
+                     const void* bias, int M, int N, int K, int epilogue, int tile, void* ws, long ws_bytes,
+                     void* stream);
 
 /* W8A8 linear (Int8DynamicLinear, int8_dit.py:34-65).
  * Per-row dynamic activation quantisation of bf16 x [M, K] in bf16 arithmetic
@@ -144,6 +155,10 @@ int dfh_quant_weight_i8(const void* w, void* q, void* scale, int N, int K, void*
  * (bias bf16 or NULL). K a multiple of 64; ldx/ldw in bytes, ldo in elements. */
 int dfh_gemm_w8a8(const void* xq, long ldx, const void* wq, long ldw, void* out, long ldo, const void* sx,
                   const void* sw, const void* bias, int M, int N, int K, int out_int32, int tile, void* stream);
+/* dfh_gemm_w8a8 with a K-split workspace (as dfh_gemm_bf16_ws); int32 sums are exact either way. */
+int dfh_gemm_w8a8_ws(const void* xq, long ldx, const void* wq, long ldw, void* out, long ldo, const void* sx,
+                     const void* sw, const void* bias, int M, int N, int K, int out_int32, int tile, void* ws,
+                     long ws_bytes, void* stream);
 
 /* Prefix K/V cache of a MeanFlow solve (per-(timestep, layer) cache of
  * cached_fm.py:82-197, FMCache / extend_cache / active_forward, restated for the

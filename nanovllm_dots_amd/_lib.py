@@ -63,13 +63,18 @@ SIGNATURES = {
     "dfh_dit_forward": (C.c_int, [vp, C.POINTER(DfhForwardArgs), vp]),
     "dfh_input_status": (C.c_int, [vp, C.POINTER(C.c_int), vp]),
     "dfh_profile_enable": (C.c_int, [vp, C.c_int]),
+    "dfh_set_ksplit": (C.c_int, [vp, C.c_int]),
     "dfh_profile_read": (C.c_int, [vp, C.POINTER(C.c_double), C.POINTER(C.c_long), C.c_int]),
     "dfh_gemm_bf16": (C.c_int, [vp, C.c_long, vp, C.c_long, vp, C.c_long, vp, C.c_int, C.c_int,
                                 C.c_int, C.c_int, C.c_int, vp]),
+    "dfh_gemm_bf16_ws": (C.c_int, [vp, C.c_long, vp, C.c_long, vp, C.c_long, vp, C.c_int, C.c_int,
+                                C.c_int, C.c_int, C.c_int, vp, C.c_long, vp]),
     "dfh_quant_act_i8": (C.c_int, [vp, C.c_long, vp, C.c_long, vp, C.c_int, C.c_int, vp]),
     "dfh_quant_weight_i8": (C.c_int, [vp, vp, vp, C.c_int, C.c_int, vp]),
     "dfh_gemm_w8a8": (C.c_int, [vp, C.c_long, vp, C.c_long, vp, C.c_long, vp, vp, vp, C.c_int, C.c_int,
                                 C.c_int, C.c_int, C.c_int, vp]),
+    "dfh_gemm_w8a8_ws": (C.c_int, [vp, C.c_long, vp, C.c_long, vp, C.c_long, vp, vp, vp, C.c_int, C.c_int,
+                                C.c_int, C.c_int, C.c_int, vp, C.c_long, vp]),
     "dfh_kvcache_create": (C.c_int, [vp, C.c_int, C.c_int, C.c_int, C.POINTER(vp)]),
     "dfh_kvcache_destroy": (C.c_int, [vp]),
     "dfh_kvcache_reset": (C.c_int, [vp, vp]),

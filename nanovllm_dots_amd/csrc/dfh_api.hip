@@ -96,6 +96,8 @@ struct DfhHandle {
   DevBuf rope_cos, rope_sin;
   DevBuf temb_in, t_hid, t_out, d_hid, d_out, cond, cond_act, mod;
   DevBuf z, zp, fin, vel, tvals;
+  DevBuf splitws;  // partial sums of K-split tiles: one 256x256 f32 tile per resident workgroup
+  bool ksplit = true;
 
   // profiling
   bool prof = false;
@@ -133,15 +135,21 @@ int check_cfg(const DfhConfig& c) {
   return 0;
 }
 
-hipError_t gemm(DfhHandle* h, int pc, const GemmArgs& a, int epi, hipStream_t s, int tile = -1) {
+hipError_t gemm(DfhHandle* h, int pc, const GemmArgs& a_in, int epi, hipStream_t s, int tile = -1) {
   prof_arm(h, pc);
+  GemmArgs a = a_in;
+  if (h->ksplit) {
+    a.ws = P<float>(h->splitws);  // K-split of the last partial round of tiles
+    a.ws_elems = (long)(h->splitws.bytes / 4);
+  }
   return gemm_bf16(a, epi, s, tile);
 }
 
 // Tile shape per GEMM role (indices of gemm_bf16's configurations), chosen from
 // measured throughput at M ~ 37k rows: 8-wave 256x256 for the wide (N=4096) and the
-// deep (K=4096) products, two 128x256 workgroups per CU for N=1024, K=1024 (their
-// epilogues overlap the other workgroup's MFMAs), 128x128 for the fused QKV.
+// deep (K=4096) products, two 128x128 workgroups per CU for N=1024, K=1024 (their
+// epilogues overlap the other workgroup's MFMAs; 256-wide tiles would leave a third
+// of the last round idle) and for the fused QKV.
 enum GemmRole { kRoleQKV, kRoleNarrow, kRoleWide };
 int tile_for(long M, int N, int K, GemmRole role) {
   if (M < 4096) return -1;  // small problems: the library heuristic
@@ -179,6 +187,12 @@ int reserve_rows(DfhHandle* h, long M, hipStream_t s) {
   DFH_CHECK(dev_alloc(h->vt_col, M * 4));
   DFH_CHECK(dev_alloc(h->fin, M * H * 2));
   DFH_CHECK(dev_alloc(h->vel, M * ld * 2));
+  if (!h->splitws.p) {
+    int dev = 0, cus = 0;
+    DFH_CHECK(hipGetDevice(&dev));
+    DFH_CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+    DFH_CHECK(dev_alloc(h->splitws, (size_t)cus * 256 * 256 * 4));
+  }
   h->cap_M = M;
   return 0;
 }
@@ -407,7 +421,7 @@ int dfh_destroy(DfhHandle* h) {
                     &h->vt, &h->row_req, &h->row_pos, &h->vt_col, &h->cu_rows, &h->cu_vt,
                     &h->hist_len, &h->counts, &h->err, &h->patch_rows, &h->seqs, &h->rope_cos, &h->rope_sin,
                     &h->temb_in, &h->t_hid, &h->t_out, &h->d_hid, &h->d_out, &h->cond,
-                    &h->cond_act, &h->mod, &h->z, &h->zp, &h->fin, &h->vel, &h->tvals};
+                    &h->cond_act, &h->mod, &h->z, &h->zp, &h->fin, &h->vel, &h->tvals, &h->splitws};
   for (DevBuf* b : bufs)
     if (b->p) (void)hipFree(b->p);
   for (hipEvent_t ev : h->ev_pool) (void)hipEventDestroy(ev);
@@ -621,6 +635,12 @@ int dfh_input_status(DfhHandle* h, int* flags, void* stream) {
   return 0;
 }
 
+int dfh_set_ksplit(DfhHandle* h, int enable) {
+  if (!h) return fail("null handle");
+  h->ksplit = enable != 0;
+  return 0;
+}
+
 int dfh_profile_enable(DfhHandle* h, int enable) {
   if (!h) return fail("null handle");
   if (enable && h->ev_pool.empty()) {
@@ -653,6 +673,11 @@ int dfh_profile_read(DfhHandle* h, double* ms, long* cnt, int n_classes) {
 
 int dfh_gemm_bf16(const void* A, long lda, const void* B, long ldb, void* C, long ldc, const void* bias,
                   int M, int N, int K, int epilogue, int tile, void* stream) {
+  return dfh_gemm_bf16_ws(A, lda, B, ldb, C, ldc, bias, M, N, K, epilogue, tile, nullptr, 0, stream);
+}
+
+int dfh_gemm_bf16_ws(const void* A, long lda, const void* B, long ldb, void* C, long ldc, const void* bias,
+                     int M, int N, int K, int epilogue, int tile, void* ws, long ws_bytes, void* stream) {
   if (!A || !B || !C) return fail("dfh_gemm_bf16: NULL pointer");
   if (epilogue != EPI_BIAS && epilogue != EPI_GELU && epilogue != EPI_F32)
     return fail("dfh_gemm_bf16: epilogue %d not exposed", epilogue);
@@ -665,6 +690,7 @@ int dfh_gemm_bf16(const void* A, long lda, const void* B, long ldb, void* C, lon
   a.C = reinterpret_cast<uint16_t*>(C); a.Cf = reinterpret_cast<float*>(C); a.ldc = ldc;
   a.bias = reinterpret_cast<const uint16_t*>(bias);
   a.M = M; a.N = N; a.K = K;
+  a.ws = reinterpret_cast<float*>(ws); a.ws_elems = ws ? ws_bytes / 4 : 0;
   hipError_t e = gemm_bf16(a, epilogue, reinterpret_cast<hipStream_t>(stream), tile);
   if (e != hipSuccess) return fail("dfh_gemm_bf16(M=%d N=%d K=%d tile=%d): %s", M, N, K, tile,
                                    hipGetErrorString(e));
@@ -692,6 +718,12 @@ int dfh_quant_weight_i8(const void* w, void* q, void* scale, int N, int K, void*
 
 int dfh_gemm_w8a8(const void* xq, long ldx, const void* wq, long ldw, void* out, long ldo, const void* sx,
                   const void* sw, const void* bias, int M, int N, int K, int out_int32, int tile, void* stream) {
+  return dfh_gemm_w8a8_ws(xq, ldx, wq, ldw, out, ldo, sx, sw, bias, M, N, K, out_int32, tile, nullptr, 0, stream);
+}
+
+int dfh_gemm_w8a8_ws(const void* xq, long ldx, const void* wq, long ldw, void* out, long ldo, const void* sx,
+                     const void* sw, const void* bias, int M, int N, int K, int out_int32, int tile, void* ws,
+                     long ws_bytes, void* stream) {
   if (!xq || !wq || !out) return fail("dfh_gemm_w8a8: NULL pointer");
   if (!out_int32 && (!sx || !sw)) return fail("dfh_gemm_w8a8: dequantised output needs both scales");
   if (K % 64 || ldx % 16 || ldw % 16 || ldx < K || ldw < K || ldo < N || ldo % 4)
@@ -704,6 +736,7 @@ int dfh_gemm_w8a8(const void* xq, long ldx, const void* wq, long ldw, void* out,
   a.sx = reinterpret_cast<const float*>(sx); a.sw = reinterpret_cast<const float*>(sw);
   a.bias = reinterpret_cast<const uint16_t*>(bias);
   a.M = M; a.N = N; a.K = K;
+  a.ws = reinterpret_cast<float*>(ws); a.ws_elems = ws ? ws_bytes / 4 : 0;
   hipError_t e = gemm_i8(a, out_int32 ? EPI_I32 : EPI_DQ, reinterpret_cast<hipStream_t>(stream), tile);
   if (e != hipSuccess)
     return fail("dfh_gemm_w8a8(M=%d N=%d K=%d tile=%d): %s", M, N, K, tile, hipGetErrorString(e));

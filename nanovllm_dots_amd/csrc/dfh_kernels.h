@@ -47,6 +47,11 @@ struct GemmArgs {
   const uint16_t* kn_w; const uint16_t* kn_b;
   uint16_t* vt; long ld_vt; const int* vt_col;   // V^T [hidden, ld_vt]; column of row m = vt_col[m]
   const int* c_rows;                             // optional: q|k output row of row m
+  // Optional K-split of the last, partial round of tiles: each XCD's leftover
+  // tiles are cut along K over its idle workgroups; partial sums go to ws and a
+  // second kernel adds them and runs the epilogue. ws_elems (32-bit words) must
+  // cover grid * BM * BN or the split is off.
+  float* ws; long ws_elems;
 };
 
 // Picks a tile shape for (M, N, K) and launches the persistent MFMA kernel.

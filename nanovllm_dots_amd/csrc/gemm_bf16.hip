@@ -75,12 +75,14 @@ __device__ __forceinline__ int lds_off(int row, int chunk) {
 // on 16-bit units for both; one 16-byte fragment is 8 bf16 or 16 int8 values.
 struct OpBf16 {
   using acc_t = floatx16;
+  using elem_t = float;
   __device__ static __forceinline__ acc_t mma(const bf16x8& a, const bf16x8& b, const acc_t& c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
   }
 };
 struct OpI8 {
   using acc_t = intx16;
+  using elem_t = int;
   __device__ static __forceinline__ acc_t mma(const bf16x8& a, const bf16x8& b, const acc_t& c) {
     return __builtin_amdgcn_mfma_i32_32x32x32_i8(__builtin_bit_cast(intx4, a), __builtin_bit_cast(intx4, b),
                                                   c, 0, 0, 0);
@@ -405,6 +407,23 @@ __device__ __forceinline__ void run_epilogue(const GemmArgs& a, ACC (&acc)[C::RN
     }
 }
 
+// K-split of an XCD's last round: chunk_x tiles over per_xcd workgroups leave
+// tail = chunk_x mod per_xcd tiles for a partial round. Cut each of them into
+// split = per_xcd / tail K pieces (at least kMinSplitSteps K steps each) so the
+// round takes 1/split of a tile instead of a whole one.
+constexpr int kMinSplitSteps = 4;
+__device__ __forceinline__ void split_plan(int chunk_x, int per_xcd, int KT, int& full_x, int& split) {
+  full_x = chunk_x;
+  split = 1;
+  const int rounds = chunk_x / per_xcd, tail = chunk_x - rounds * per_xcd;
+  if (tail == 0) return;
+  int sp = per_xcd / tail;
+  if (sp > KT / kMinSplitSteps) sp = KT / kMinSplitSteps;
+  if (sp < 2) return;
+  full_x = rounds * per_xcd;
+  split = sp;
+}
+
 template <class C, class Op, int EPI>
 __global__ void __launch_bounds__(C::THREADS, C::WAVES_PER_EU)
 gemm_mfma_kernel(GemmArgs a) {
@@ -449,7 +468,13 @@ gemm_mfma_kernel(GemmArgs a) {
   const int slot = blockIdx.x / nxcd;
   const int per_xcd = gridDim.x / nxcd;
   const int chunk = (total + nxcd - 1) / nxcd;
-  auto tile_at = [&](int jt) { const int t = xcd * chunk + jt; return (jt < chunk && t < total) ? t : -1; };
+  // Work of this workgroup: whole tiles jt = slot, slot + per_xcd, ... < full_x
+  // of the XCD's chunk, then (split > 1) one K piece of a leftover tile.
+  int chunk_x = total - xcd * chunk;
+  chunk_x = chunk_x < 0 ? 0 : (chunk_x > chunk ? chunk : chunk_x);
+  int full_x = chunk_x, split = 1;
+  if (a.ws != nullptr) split_plan(chunk_x, per_xcd, K / BK, full_x, split);
+  auto tile_at = [&](int jt) { return jt < full_x ? xcd * chunk + jt : -1; };
   // Grouped order: the per_xcd tiles an XCD runs at once cover GM row blocks x
   // per_xcd/GM column blocks (row block fastest), so each A row block and W
   // column block is fetched into that XCD's L2 once per round, not per tile.
@@ -534,41 +559,56 @@ gemm_mfma_kernel(GemmArgs a) {
   };
 
   const int KT = K / BK;
+  int kb = 0, KTi = KT;  // K steps [kb, kb + KTi) of the current work item
   // Vector-memory ops decrement vmcnt in issue order. The epilogue issues
   // exactly kEpiStores stores after the next tile's prologue DMA, so that
   // tile's first step waits for vmcnt <= kEpiStores (+ the later prologue
   // stages) and leaves the stores in flight. The QKV epilogue (data-dependent
   // store count) waits for zero.
-  constexpr int kEpiStores = (EPI == EPI_QKV) ? -1 : Staged<C, EPI>::value ? Staged<C, EPI>::kStores
-                                                                          : C::RN * C::RM * 4;
-  constexpr int kStartWait = (ST >= 2 ? (ST - 2) * C::LPS : 0) + (kEpiStores > 0 ? kEpiStores : 0);
+  constexpr int kEpiStoresRaw = (EPI == EPI_QKV) ? -1 : Staged<C, EPI>::value ? Staged<C, EPI>::kStores
+                                                                             : C::RN * C::RM * 4;
+  constexpr int kWaitBase = ST >= 2 ? (ST - 2) * C::LPS : 0;
+  // vmcnt holds at most 63: larger counts fall back to a full wait
+  constexpr int kEpiStores = kWaitBase + kEpiStoresRaw < 64 ? kEpiStoresRaw : -1;
+  constexpr int kStartWait = kWaitBase + (kEpiStores > 0 ? kEpiStores : 0);
   static_assert(kStartWait < 64, "vmcnt range");
   // one pipelined K step: k = step index, stage s = k % ST (compile-time)
+  // one pipelined K step: k = step index within the item, stage s = k % ST (compile-time)
   auto step = [&](auto stc, int k) {
     constexpr int s = decltype(stc)::value;
-    if (k >= KT) return;  // uniform
+    if (k >= KTi) return;  // uniform
     if (k == 0) {
       if constexpr (kEpiStores >= 0 && ST == 2) {
         wait_vm_lgkm0<kStartWait>();
       } else if constexpr (kEpiStores >= 0) {
-        if (KT >= ST - 1) wait_vm_lgkm0<(kEpiStores >= 0 ? kStartWait : 0)>();
+        if (KTi >= ST - 1) wait_vm_lgkm0<(kEpiStores >= 0 ? kStartWait : 0)>();
         else wait_vm_lgkm0<0>();
       } else {
         wait_vm_lgkm0<0>();
       }
-    } else if (k + ST - 2 >= KT) {
+    } else if (k + ST - 2 >= KTi) {
       wait_vm_lgkm0<0>();   // pipeline drain: exact
     } else {
       wait_vm_lgkm0<(ST >= 2 ? (ST - 2) * C::LPS : 0)>();
     }
     __builtin_amdgcn_s_barrier();
-    if (k + ST - 1 < KT) dma(std::integral_constant<int, (s + ST - 1) % ST>{}, k + ST - 1);
+    if (k + ST - 1 < KTi) dma(std::integral_constant<int, (s + ST - 1) % ST>{}, kb + k + ST - 1);
     compute(stc);
   };
   auto prologue = [&]() {
-    dma(std::integral_constant<int, 0>{}, 0);
-    if constexpr (ST > 2) { if (1 < KT) dma(std::integral_constant<int, 1 % ST>{}, 1); }
-    if constexpr (ST > 3) { if (2 < KT) dma(std::integral_constant<int, 2 % ST>{}, 2); }
+    dma(std::integral_constant<int, 0>{}, kb);
+    if constexpr (ST > 2) { if (1 < KTi) dma(std::integral_constant<int, 1 % ST>{}, kb + 1); }
+    if constexpr (ST > 3) { if (2 < KTi) dma(std::integral_constant<int, 2 % ST>{}, kb + 2); }
+  };
+  // the K piece of a leftover tile this workgroup runs last (piece < 0: none)
+  const int tail_tiles = chunk_x - full_x;
+  const int piece = (split > 1 && slot < tail_tiles * split) ? slot : -1;
+  auto set_item = [&](int jt_or_piece, bool is_piece) -> int {  // returns the tile, sets kb / KTi
+    if (!is_piece) { kb = 0; KTi = KT; return xcd * chunk + jt_or_piece; }
+    const int kc = jt_or_piece % split;
+    kb = kc * KT / split;
+    KTi = (kc + 1) * KT / split - kb;
+    return xcd * chunk + full_x + jt_or_piece / split;
   };
 
   int jt = slot;
@@ -617,6 +657,109 @@ gemm_mfma_kernel(GemmArgs a) {
     }
     tile = next;
   }
+  if (piece < 0) return;
+  // One K piece of a leftover tile: partial sums to the workspace in MFMA lane
+  // layout, one 16-B store per (wave, i, k, quarter, lane); the reduce kernel
+  // adds the pieces and runs the epilogue.
+  set_offsets(set_item(piece, true));
+  prologue();
+  wait_vm_lgkm0<0>();
+#pragma unroll
+  for (int i = 0; i < C::RN; ++i)
+#pragma unroll
+    for (int k = 0; k < C::RM; ++k)
+#pragma unroll
+      for (int t = 0; t < 16; ++t) acc[i][k][t] = 0;
+  for (int k0 = 0; k0 < KTi; k0 += ST) {
+    step(std::integral_constant<int, 0>{}, k0);
+    if constexpr (ST > 1) step(std::integral_constant<int, 1 % ST>{}, k0 + 1);
+    if constexpr (ST > 2) step(std::integral_constant<int, 2 % ST>{}, k0 + 2);
+    if constexpr (ST > 3) step(std::integral_constant<int, 3 % ST>{}, k0 + 3);
+  }
+  float* wp = a.ws + (long)(xcd * per_xcd + piece) * (BM * BN);
+#pragma unroll
+  for (int i = 0; i < C::RN; ++i)
+#pragma unroll
+    for (int k = 0; k < C::RM; ++k)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const long e = ((((long)wave * C::RN + i) * C::RM + k) * 4 + q) * 64 + lane;
+        // copy the elements out first: a bit_cast of a vector-element expression reads element 0
+        using E = typename Op::elem_t;
+        const E e0 = acc[i][k][4 * q], e1 = acc[i][k][4 * q + 1], e2 = acc[i][k][4 * q + 2],
+                e3 = acc[i][k][4 * q + 3];
+        *reinterpret_cast<float4*>(wp + e * 4) =
+            make_float4(__builtin_bit_cast(float, e0), __builtin_bit_cast(float, e1), __builtin_bit_cast(float, e2),
+                        __builtin_bit_cast(float, e3));
+      }
+}
+
+// Second half of the K-split: one single-wave workgroup per (split tile, wave
+// sub-tile) of the GEMM's tile walk, so all CUs share the reduction. It adds the
+// pieces' partial sums in piece order and runs that wave's part of the tile
+// epilogue with the same code as the GEMM kernel. Grid: 8 * per_xcd * NW.
+template <class C, class Op, int EPI>
+__global__ void __launch_bounds__(64)
+gemm_split_reduce_kernel(GemmArgs a, int per_xcd) {
+  constexpr int BM = C::BM, BN = C::BN, BK = C::BK;
+  __shared__ __attribute__((aligned(1024))) uint16_t stage_buf[Staged<C, EPI>::value ? 32 * C::WTN : 8];
+  const int M = a.M_dev ? *a.M_dev : a.M;
+  const int tiles_m = (M + BM - 1) / BM, tiles_n = a.N / BN;
+  const int total = tiles_m * tiles_n;
+  const int nxcd = 8, xcd = blockIdx.x % nxcd, r = blockIdx.x / nxcd;
+  const int slot = r / C::NW, wave = r % C::NW;
+  const int chunk = (total + nxcd - 1) / nxcd;
+  int chunk_x = total - xcd * chunk;
+  chunk_x = chunk_x < 0 ? 0 : (chunk_x > chunk ? chunk : chunk_x);
+  int full_x, split;
+  split_plan(chunk_x, per_xcd, a.K / BK, full_x, split);
+  if (split < 2 || slot >= chunk_x - full_x) return;  // uniform
+  const int tile = xcd * chunk + full_x + slot;
+  const int gn = tiles_n < 8 ? tiles_n : 8;
+  const int GM = per_xcd / gn > 1 ? per_xcd / gn : 1;
+  const int gsz = GM * tiles_n;
+  const int g = tile / gsz, w = tile - g * gsz, gm0 = g * GM;
+  const int rows = tiles_m - gm0 < GM ? tiles_m - gm0 : GM;
+  const int m0 = (gm0 + w % rows) * BM, n0 = (w / rows) * BN;
+
+  const int lane = threadIdx.x;
+  const int wm = wave / C::WN, wn = wave % C::WN;
+  const int l32 = lane & 31, hi = lane >> 5;
+  using E = typename Op::elem_t;
+  typename Op::acc_t acc[C::RN][C::RM];
+  for (int kc = 0; kc < split; ++kc) {
+    const float* wp = a.ws + (long)(xcd * per_xcd + slot * split + kc) * (BM * BN);
+    float4 v[C::RN][C::RM][4];
+#pragma unroll
+    for (int i = 0; i < C::RN; ++i)
+#pragma unroll
+      for (int k = 0; k < C::RM; ++k)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const long e = ((((long)wave * C::RN + i) * C::RM + k) * 4 + q) * 64 + lane;
+          v[i][k][q] = *reinterpret_cast<const float4*>(wp + e * 4);
+        }
+#pragma unroll
+    for (int i = 0; i < C::RN; ++i)
+#pragma unroll
+      for (int k = 0; k < C::RM; ++k)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const float f[4] = {v[i][k][q].x, v[i][k][q].y, v[i][k][q].z, v[i][k][q].w};
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            const E x = __builtin_bit_cast(E, f[t]);
+            acc[i][k][4 * q + t] = kc == 0 ? x : acc[i][k][4 * q + t] + x;
+          }
+        }
+  }
+  if constexpr (Staged<C, EPI>::value) {
+    StagedOperands<C, EPI> sop;
+    staged_preload<C, EPI>(a, sop, m0, n0, M, wm, wn, l32, hi);
+    staged_epilogue<C, EPI>(a, acc, sop, m0, n0, M, wm, wn, lane, l32, hi, stage_buf);
+  } else {
+    run_epilogue<C, EPI>(a, acc, m0, n0, M, wm, wn, l32, hi);
+  }
 }
 
 int g_num_cus = 0;
@@ -633,13 +776,20 @@ int num_cus() {
 }
 
 template <class C, class Op, int EPI>
-hipError_t launch(const GemmArgs& a, hipStream_t s) {
+hipError_t launch(const GemmArgs& a_in, hipStream_t s) {
   auto kern = gemm_mfma_kernel<C, Op, EPI>;
-  const long tiles_upper = (long)((a.M + C::BM - 1) / C::BM) * (a.N / C::BN);
+  const long tiles_upper = (long)((a_in.M + C::BM - 1) / C::BM) * (a_in.N / C::BN);
   long grid = (long)num_cus() * C::WG_PER_CU;
   if (tiles_upper < grid) grid = ((tiles_upper + 7) / 8) * 8;
   if (grid < 8) grid = 8;
+  GemmArgs a = a_in;
+  // the K-split needs a workspace slot per workgroup; QKV keeps whole tiles
+  if (a.ws && (EPI == EPI_QKV || a.ws_elems < grid * C::BM * C::BN)) a.ws = nullptr;
   dfh_launch(kern, dim3((unsigned)grid), dim3(C::THREADS), 0, s, a);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || !a.ws) return e;
+  dfh_launch(gemm_split_reduce_kernel<C, Op, EPI>, dim3((unsigned)(grid * C::NW)), dim3(64), 0, s, a,
+             (int)(grid / 8));
   return hipGetLastError();
 }
 

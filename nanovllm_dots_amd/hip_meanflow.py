@@ -224,6 +224,10 @@ class HipFMHead:
         _lib.check(self.lib.dfh_reserve(self.handle, n, total_len, num_steps, _lib.stream_ptr()),
                    "dfh_reserve")
 
+    def set_ksplit(self, enable: bool) -> None:
+        """K-split of each GEMM's last partial round of tiles (on by default)."""
+        _lib.check(self.lib.dfh_set_ksplit(self.handle, int(enable)), "dfh_set_ksplit")
+
     def profile(self, enable: bool) -> None:
         _lib.check(self.lib.dfh_profile_enable(self.handle, int(enable)), "dfh_profile_enable")
 

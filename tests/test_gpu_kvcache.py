@@ -109,3 +109,28 @@ def test_full_size_long_prefix():
     cache.extend(_pad(prefix, cfg.hidden).cuda(), [p.shape[0] for p in prefix])
     got = cache.solve(torch.stack([h[-1] for h in hist]).cuda(), noise=noise.cuda())
     _check(got, ref, cfg.latent_dim, "full-size cached")
+
+
+@pytest.mark.parametrize("path", ["direct", "cached"])
+def test_ksplit_matches_whole_tiles(path):
+    """The K-split of the last partial round of GEMM tiles against whole tiles
+    (float32 partial sums in piece order: agreement to bf16 rounding)."""
+    from nanovllm_dots_amd import HipFMCache, HipMeanflow
+    head, _ = _head(CFG, 8)
+    lens, hist, noise = R.synthetic_requests(4, 5, 260, CFG, seed=11)
+    bf = lambda t: t.to("cuda", torch.bfloat16)
+    outs = []
+    for ks in (False, True):
+        head.set_ksplit(ks)
+        if path == "direct":
+            inp, mask, pos, g = R.pack_fm_inputs(hist, CFG.patch, CFG.hidden)
+            out = HipMeanflow(None, num_steps=4, dit=object(), head=head)(
+                input_sequence=bf(inp), attn_mask=None, pos_ids=pos.cuda(), g_cond=bf(g), noise=bf(noise))
+        else:
+            cache = HipFMCache(head, 4, max(lens) + 24, 4)
+            prefix = [h[:-1] for h in hist]
+            cache.extend(_pad(prefix, CFG.hidden).cuda(), [p.shape[0] for p in prefix])
+            out = cache.solve(torch.stack([h[-1] for h in hist]).cuda(), noise=bf(noise))
+        outs.append(out)
+    head.set_ksplit(True)
+    _check(outs[1], outs[0], CFG.latent_dim, f"ksplit-vs-whole {path}")

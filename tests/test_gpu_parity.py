@@ -249,3 +249,35 @@ def test_full_size_nfe4_solve():
     got = mf(input_sequence=_cuda_bf16(inp), attn_mask=None, pos_ids=pos.cuda(), g_cond=_cuda_bf16(g),
              noise=_cuda_bf16(noise))
     _assert_latents(got, ref, cfg.latent_dim, "full-nfe4")
+
+
+@pytest.mark.parametrize("M,K,N,tile,epi", [(36937, 4096, 1024, 0, 4), (36937, 1024, 4096, 0, 1),
+                                            (3000, 2048, 256, 3, 4), (700, 1024, 256, 3, 0)])
+def test_gemm_ksplit_matches_whole_tiles(M, K, N, tile, epi):
+    """bf16 GEMM with the K-split workspace vs without (float32 sums in a
+    different order: f32 output to 1e-5 relative, bf16 output to one ulp)."""
+    from nanovllm_dots_amd import _lib
+    lib = _lib.lib()
+    g = torch.Generator(device="cpu").manual_seed(M + N)
+    A = torch.randn(M, K, generator=g).bfloat16().cuda()
+    B = (0.02 * torch.randn(N, K, generator=g)).bfloat16().cuda()
+    bias = (0.1 * torch.randn(N, generator=g)).bfloat16().cuda()
+    dt = torch.float32 if epi == 4 else torch.bfloat16
+    ws = torch.empty(1 << 26, dtype=torch.uint8, device="cuda")
+    outs = []
+    for use_ws in (False, True):
+        C = torch.zeros((M, N), device="cuda", dtype=dt)
+        print(f"gemm ksplit M={M} K={K} N={N} tile={tile} epi={epi} ws={use_ws}", flush=True)
+        _lib.check(lib.dfh_gemm_bf16_ws(_lib.ptr(A), K, _lib.ptr(B), K, _lib.ptr(C), N, _lib.ptr(bias), M, N, K,
+                                        epi, tile, _lib.ptr(ws) if use_ws else None, ws.numel() if use_ws else 0,
+                                        _lib.stream_ptr()), "dfh_gemm_bf16_ws")
+        outs.append(C.float().cpu())
+    whole, split = outs
+    if epi == 4:
+        assert torch.allclose(split, whole, rtol=1e-5, atol=1e-5 * whole.abs().max().item())
+    else:
+        # one f32 ulp of the sum can flip the bf16 rounding of the (pre-activation) value:
+        # a bf16 ulp of the pre-activation (through GELU' <= 1.13) plus one of the output
+        pre = (A.float() @ B.float().t() + bias.float()).abs().cpu()
+        tol = pre * 2.0 ** -7 * 1.2 + whole.abs() * 2.0 ** -8 + 1e-6
+        assert ((split - whole).abs() <= tol).all()

@@ -127,3 +127,25 @@ def test_quantize_dit_swaps_eligible_linears():
     assert isinstance(net[0], HipInt8Linear) and isinstance(net[2], torch.nn.Linear)
     out = net(torch.randn(20, 1024, device="cuda", dtype=torch.bfloat16))
     assert out.shape == (20, 64) and torch.isfinite(out.float()).all()
+
+
+def _split_ws():
+    return torch.empty(1 << 26, dtype=torch.uint8, device="cuda")  # 64 MiB: one 256x256 f32 tile per CU
+
+
+@pytest.mark.parametrize("M,K,N,tile", [(36937, 4096, 1024, 0), (36937, 1024, 4096, 0), (3000, 2048, 256, 3)])
+def test_int32_ksplit_exact(M, K, N, tile):
+    """K-split of the last partial tile round: int32 partial sums add exactly."""
+    from nanovllm_dots_amd import _lib
+    lib = _lib.lib()
+    g = torch.Generator(device="cpu").manual_seed(M + K)
+    xq = torch.randint(-127, 128, (M, K), generator=g, dtype=torch.int8).cuda()
+    wq = torch.randint(-127, 128, (N, K), generator=g, dtype=torch.int8).cuda()
+    ws = _split_ws()
+    out = torch.empty((M, N), device="cuda", dtype=torch.int32)
+    print(f"w8a8 ksplit M={M} K={K} N={N} tile={tile}", flush=True)
+    _lib.check(lib.dfh_gemm_w8a8_ws(_lib.ptr(xq), K, _lib.ptr(wq), K, _lib.ptr(out), N, None, None, None, M, N, K,
+                                    1, tile, _lib.ptr(ws), ws.numel(), _lib.stream_ptr()), "dfh_gemm_w8a8_ws")
+    ref = torch._int_mm(xq, wq.t().contiguous())
+    bad = (out != ref).nonzero()
+    assert bad.numel() == 0, f"{bad.shape[0]} mismatches, first rows {bad[:4].tolist()}"
