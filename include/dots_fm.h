@@ -122,7 +122,7 @@ int dfh_input_status(DfhHandle* h, int* flags, void* stream);
 
 /* Per-kernel-class timing with dispatch-packet events (bench instrumentation).
  * classes: 0 qkv gemm, 1 o_proj gemm, 2 fc1 gemm, 3 fc2 gemm, 4 attention,
- * 5 ln_modulate, 6 other. */
+ * 5 ln_modulate, 6 other, 7/8/9 the K-split reduce of o_proj / fc1 / fc2. */
 int dfh_profile_enable(DfhHandle* h, int enable);
 /* K-split of each GEMM's last, partial round of tiles (default on): leftover
  * tiles are cut along K over the idle workgroups, with a second kernel that

@@ -11,6 +11,8 @@ struct LaunchEvents {
   hipEvent_t start = nullptr, stop = nullptr;
 };
 extern thread_local LaunchEvents g_launch_events;
+// a second armed pair for a follow-up launch of the same operation (K-split reduce)
+extern thread_local LaunchEvents g_launch_events_aux;
 
 // launch helper honouring g_launch_events
 template <typename K, typename... Args>
@@ -107,13 +109,22 @@ hipError_t decode_attention(const uint16_t* qk, long ldqk, const uint16_t* vt, l
 #include <hip/hip_ext.h>
 namespace dfh {
 template <typename K, typename... Args>
-inline void dfh_launch(K kernel, dim3 grid, dim3 block, unsigned shmem, hipStream_t s, Args... args) {
-  if (g_launch_events.start) {
-    hipEvent_t a = g_launch_events.start, b = g_launch_events.stop;
-    g_launch_events.start = g_launch_events.stop = nullptr;
+inline void dfh_launch_with(LaunchEvents& ev, K kernel, dim3 grid, dim3 block, unsigned shmem, hipStream_t s,
+                            Args... args) {
+  if (ev.start) {
+    hipEvent_t a = ev.start, b = ev.stop;
+    ev.start = ev.stop = nullptr;
     hipExtLaunchKernelGGL(kernel, grid, block, shmem, s, a, b, 0, args...);
   } else {
     hipLaunchKernelGGL(kernel, grid, block, shmem, s, args...);
   }
+}
+template <typename K, typename... Args>
+inline void dfh_launch(K kernel, dim3 grid, dim3 block, unsigned shmem, hipStream_t s, Args... args) {
+  dfh_launch_with(g_launch_events, kernel, grid, block, shmem, s, args...);
+}
+template <typename K, typename... Args>
+inline void dfh_launch_aux(K kernel, dim3 grid, dim3 block, unsigned shmem, hipStream_t s, Args... args) {
+  dfh_launch_with(g_launch_events_aux, kernel, grid, block, shmem, s, args...);
 }
 }  // namespace dfh

@@ -787,10 +787,14 @@ hipError_t launch(const GemmArgs& a_in, hipStream_t s) {
   if (a.ws && (EPI == EPI_QKV || a.ws_elems < grid * C::BM * C::BN)) a.ws = nullptr;
   dfh_launch(kern, dim3((unsigned)grid), dim3(C::THREADS), 0, s, a);
   hipError_t e = hipGetLastError();
-  if (e != hipSuccess || !a.ws) return e;
-  dfh_launch(gemm_split_reduce_kernel<C, Op, EPI>, dim3((unsigned)(grid * C::NW)), dim3(64), 0, s, a,
-             (int)(grid / 8));
-  return hipGetLastError();
+  if constexpr (EPI == EPI_QKV) {
+    return e;
+  } else {
+    if (e != hipSuccess || !a.ws) return e;
+    dfh_launch_aux(gemm_split_reduce_kernel<C, Op, EPI>, dim3((unsigned)(grid * C::NW)), dim3(64), 0, s, a,
+                   (int)(grid / 8));
+    return hipGetLastError();
+  }
 }
 
 // tile configurations: (BM, BN, BK, stages, wave grid)
