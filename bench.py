@@ -8,8 +8,8 @@ weights N(0, 0.02), contexts N(0,1), noise N(0,1), g_cond = 0.
 Prints one JSON line:
   value        DiT GEMM TFLOP/s = 12 * 2*M*(4H^2 + 2HF) * NFE / wall-per-solve,
                M = sum(c_i + 16) unpadded rows
-  roofline     the dominant GEMM (largest total time, its K-split reduce included)
-               timed with dispatch-packet HIP events inside the timed region
+  roofline     the dominant GEMM (largest total time) timed with dispatch-packet
+               HIP events inside the timed region
   cpu_baseline the oracle's float32 DiT on the host cores over a bounded
                sample of the same workload (first k requests, full NFE=4 solve)
 
@@ -40,9 +40,8 @@ def log(*a):
 
 
 def pmc_traffic(role: str):
-    """HBM bytes per launch of ``role`` (its K-split reduce included) from the
-    committed FETCH_SIZE/WRITE_SIZE summary of this workload (two rocprofv3 --pmc
-    runs, copy-calibrated), or None."""
+    """HBM bytes per launch of ``role`` from the committed FETCH_SIZE/WRITE_SIZE
+    summary of this workload (two rocprofv3 --pmc runs, copy-calibrated), or None."""
     found = {}
     try:
         for line in open(TRAFFIC_PROFILE):
@@ -51,9 +50,7 @@ def pmc_traffic(role: str):
                 found[f[1]] = int(f[2])
     except OSError:
         return None
-    if role not in found:
-        return None
-    return found[role] + found.get(role + "_splitk", 0)
+    return found.get(role)
 
 
 def cpu_baseline(cfg, W, lens, hist, noise, budget_s: float):
@@ -266,11 +263,9 @@ def main():
                   "fc1_gemm": 2 * (M * H + F * H + M * F),
                   "fc2_gemm": 2 * (M * F + F * H + 2 * M * H)}
     classes = {k: v for k, v in prof.items()}
-    # a GEMM's time includes the K-split reduce of its last partial round of tiles
-    role_ms = {k: classes[k][0] + classes.get(k + "_splitk", (0.0, 0))[0] for k in per_launch}
+    role_ms = {k: classes[k][0] for k in per_launch}
     dom = max(per_launch, key=lambda k: role_ms[k])
     dom_n = classes[dom][1]
-    gemm_kernel_ms = classes[dom][0] / max(dom_n, 1)
     avg_ms = role_ms[dom] / max(dom_n, 1)
     achieved = per_launch[dom] / (avg_ms * 1e-3) / 1e12
     breakdown = {k: {"ms_per_solve": v[0] / args.steps, "launches_per_solve": v[1] / args.steps}
@@ -303,8 +298,7 @@ def main():
                      "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": pmc_traffic(dom),
                      "traffic_unit": "bytes/launch", "algorithmic_bytes": algo_bytes[dom],
-                     "avg_launch_ms": round(avg_ms, 5), "gemm_kernel_ms": round(gemm_kernel_ms, 5),
-                     "splitk_reduce_ms": round(avg_ms - gemm_kernel_ms, 5), "flops_per_launch": per_launch[dom]},
+                     "avg_launch_ms": round(avg_ms, 5), "flops_per_launch": per_launch[dom]},
         "kernel_breakdown": breakdown,
         "w8a8_m16384": w8,
         "kvcache_4x10111": kvc,

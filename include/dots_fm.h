@@ -122,11 +122,11 @@ int dfh_input_status(DfhHandle* h, int* flags, void* stream);
 
 /* Per-kernel-class timing with dispatch-packet events (bench instrumentation).
  * classes: 0 qkv gemm, 1 o_proj gemm, 2 fc1 gemm, 3 fc2 gemm, 4 attention,
- * 5 ln_modulate, 6 other, 7/8/9 the K-split reduce of o_proj / fc1 / fc2. */
+ * 5 ln_modulate, 6 other. */
 int dfh_profile_enable(DfhHandle* h, int enable);
 /* K-split of each GEMM's last, partial round of tiles (default on): leftover
- * tiles are cut along K over the idle workgroups, with a second kernel that
- * adds the partial sums. Off: every tile runs whole. No reference counterpart
+ * tiles are cut along K over the idle workgroups; the workgroup that completes a
+ * tile adds the partial sums. Off: every tile runs whole. No reference counterpart
  * (a scheduling choice of this library; results agree to float32 summation order). */
 int dfh_set_ksplit(DfhHandle* h, int enable);
 int dfh_profile_read(DfhHandle* h, double* ms_per_class, long* launches_per_class, int n_classes);
@@ -137,7 +137,9 @@ int dfh_gemm_bf16(const void* A, long lda, const void* B, long ldb, void* C, lon
                   const void* bias, int M, int N, int K, int epilogue, int tile, void* stream);
 /* dfh_gemm_bf16 with a device workspace (ws, ws_bytes) for the K-split of the
  * last partial round of tiles (see dfh_set_ksplit); too small or NULL: no split.
- * ws_bytes >= 4 * 65536 * (number of CUs) always suffices. */
+ * ws_bytes >= 4 * (4096 + 65536 * (number of CUs)) always suffices. The workspace must be
+ * zero-filled before its first use; calls leave it reusable (its tile counters
+ * return to zero). Calls sharing one workspace must not overlap. */
 int dfh_gemm_bf16_ws(const void* A, long lda, const void* B, long ldb, void* C, long ldc,
                      const void* bias, int M, int N, int K, int epilogue, int tile, void* ws, long ws_bytes,
                      void* stream);

@@ -22,7 +22,6 @@
 
 namespace dfh {
 thread_local LaunchEvents g_launch_events;
-thread_local LaunchEvents g_launch_events_aux;
 }
 
 using namespace dfh;
@@ -71,8 +70,7 @@ hipError_t dev_alloc(DevBuf& b, size_t bytes) {
 template <typename T>
 T* P(DevBuf& b) { return reinterpret_cast<T*>(b.p); }
 
-enum ProfClass { PC_QKV = 0, PC_O, PC_FC1, PC_FC2, PC_ATTN, PC_LN, PC_OTHER, PC_O_SPLITK, PC_FC1_SPLITK,
-                 PC_FC2_SPLITK, PC_N };
+enum ProfClass { PC_QKV = 0, PC_O, PC_FC1, PC_FC2, PC_ATTN, PC_LN, PC_OTHER, PC_N };
 
 }  // namespace
 
@@ -98,7 +96,7 @@ struct DfhHandle {
   DevBuf rope_cos, rope_sin;
   DevBuf temb_in, t_hid, t_out, d_hid, d_out, cond, cond_act, mod;
   DevBuf z, zp, fin, vel, tvals;
-  DevBuf splitws;  // partial sums of K-split tiles: one 256x256 f32 tile per resident workgroup
+  DevBuf splitws;  // K-split: tile counters, then a 256x256 f32 partial tile per resident workgroup
   bool ksplit = true;
 
   // profiling
@@ -113,16 +111,15 @@ struct DfhHandle {
 namespace {
 
 // arm dispatch-packet events for the next launch of class `pc`
-void prof_arm_slot(DfhHandle* h, int pc, LaunchEvents& slot) {
+void prof_arm(DfhHandle* h, int pc) {
   if (!h->prof) return;
   if (h->ev_next + 2 > h->ev_pool.size()) return;  // pool full: drop the sample
   const int i = (int)h->ev_next;
   h->ev_next += 2;
-  slot.start = h->ev_pool[i];
-  slot.stop = h->ev_pool[i + 1];
+  g_launch_events.start = h->ev_pool[i];
+  g_launch_events.stop = h->ev_pool[i + 1];
   h->ev_used.push_back({pc, i});
 }
-void prof_arm(DfhHandle* h, int pc) { prof_arm_slot(h, pc, g_launch_events); }
 
 int check_cfg(const DfhConfig& c) {
   if (c.head_dim != 64) return fail("head_dim must be 64 (got %d)", c.head_dim);
@@ -141,19 +138,11 @@ int check_cfg(const DfhConfig& c) {
 hipError_t gemm(DfhHandle* h, int pc, const GemmArgs& a_in, int epi, hipStream_t s, int tile = -1) {
   prof_arm(h, pc);
   GemmArgs a = a_in;
-  if (h->ksplit && a.M >= 4096) {  // small passes are launch-bound: no second kernel
+  if (h->ksplit) {
     a.ws = P<float>(h->splitws);  // K-split of the last partial round of tiles
     a.ws_elems = (long)(h->splitws.bytes / 4);
-    const int aux = pc == PC_O ? PC_O_SPLITK : pc == PC_FC1 ? PC_FC1_SPLITK : pc == PC_FC2 ? PC_FC2_SPLITK : pc;
-    prof_arm_slot(h, aux, g_launch_events_aux);  // timed only if the reduce kernel runs
   }
-  const hipError_t e = gemm_bf16(a, epi, s, tile);
-  if (g_launch_events_aux.start) {  // no reduce launched: drop the sample
-    g_launch_events_aux.start = g_launch_events_aux.stop = nullptr;
-    h->ev_used.pop_back();
-    h->ev_next -= 2;
-  }
-  return e;
+  return gemm_bf16(a, epi, s, tile);
 }
 
 // Tile shape per GEMM role (indices of gemm_bf16's configurations), chosen from
@@ -202,7 +191,8 @@ int reserve_rows(DfhHandle* h, long M, hipStream_t s) {
     int dev = 0, cus = 0;
     DFH_CHECK(hipGetDevice(&dev));
     DFH_CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
-    DFH_CHECK(dev_alloc(h->splitws, (size_t)cus * 256 * 256 * 4));
+    // 4096 tile counters, then one 256x256 f32 partial tile per resident workgroup (zeroed)
+    DFH_CHECK(dev_alloc(h->splitws, ((size_t)4096 + (size_t)cus * 256 * 256) * 4));
   }
   h->cap_M = M;
   return 0;

@@ -11,8 +11,6 @@ struct LaunchEvents {
   hipEvent_t start = nullptr, stop = nullptr;
 };
 extern thread_local LaunchEvents g_launch_events;
-// a second armed pair for a follow-up launch of the same operation (K-split reduce)
-extern thread_local LaunchEvents g_launch_events_aux;
 
 // launch helper honouring g_launch_events
 template <typename K, typename... Args>
@@ -50,9 +48,11 @@ struct GemmArgs {
   uint16_t* vt; long ld_vt; const int* vt_col;   // V^T [hidden, ld_vt]; column of row m = vt_col[m]
   const int* c_rows;                             // optional: q|k output row of row m
   // Optional K-split of the last, partial round of tiles: each XCD's leftover
-  // tiles are cut along K over its idle workgroups; partial sums go to ws and a
-  // second kernel adds them and runs the epilogue. ws_elems (32-bit words) must
-  // cover grid * BM * BN or the split is off.
+  // tiles are cut along K over its idle workgroups; partial sums go to ws and the
+  // workgroup that completes a tile adds them and runs the epilogue. ws_elems
+  // (32-bit words) must cover 4096 + grid * BM * BN or the split is off; the
+  // first 4096 words are tile counters that must be zero before the first use
+  // (they are left at zero).
   float* ws; long ws_elems;
 };
 
@@ -123,8 +123,5 @@ template <typename K, typename... Args>
 inline void dfh_launch(K kernel, dim3 grid, dim3 block, unsigned shmem, hipStream_t s, Args... args) {
   dfh_launch_with(g_launch_events, kernel, grid, block, shmem, s, args...);
 }
-template <typename K, typename... Args>
-inline void dfh_launch_aux(K kernel, dim3 grid, dim3 block, unsigned shmem, hipStream_t s, Args... args) {
-  dfh_launch_with(g_launch_events_aux, kernel, grid, block, shmem, s, args...);
-}
+
 }  // namespace dfh

@@ -412,6 +412,10 @@ __device__ __forceinline__ void run_epilogue(const GemmArgs& a, ACC (&acc)[C::RN
 // split = per_xcd / tail K pieces (at least kMinSplitSteps K steps each) so the
 // round takes 1/split of a tile instead of a whole one.
 constexpr int kMinSplitSteps = 4;
+// workspace layout: kSplitCounters 32-bit tile counters (index xcd * per_xcd +
+// leftover tile; at a fixed place for every tile shape, zero between calls),
+// then one BM x BN float32 partial tile per workgroup
+constexpr long kSplitCounters = 4096;
 __device__ __forceinline__ void split_plan(int chunk_x, int per_xcd, int KT, int& full_x, int& split) {
   full_x = chunk_x;
   split = 1;
@@ -434,6 +438,7 @@ gemm_mfma_kernel(GemmArgs a) {
   __shared__ __attribute__((aligned(1024))) uint16_t sA1[ST > 1 ? BM * BK : 8], sB1[ST > 1 ? BN * BK : 8];
   __shared__ __attribute__((aligned(1024))) uint16_t sA2[ST > 2 ? BM * BK : 8], sB2[ST > 2 ? BN * BK : 8];
   __shared__ __attribute__((aligned(1024))) uint16_t sA3[ST > 3 ? BM * BK : 8], sB3[ST > 3 ? BN * BK : 8];
+  __shared__ int s_flag;  // K-split: this workgroup completed its tile
   auto stA = [&](auto stc) -> uint16_t* {
     constexpr int s = decltype(stc)::value;
     if constexpr (s == 0) return sA0;
@@ -658,10 +663,15 @@ gemm_mfma_kernel(GemmArgs a) {
     tile = next;
   }
   if (piece < 0) return;
-  // One K piece of a leftover tile: partial sums to the workspace in MFMA lane
-  // layout, one 16-B store per (wave, i, k, quarter, lane); the reduce kernel
-  // adds the pieces and runs the epilogue.
-  set_offsets(set_item(piece, true));
+  // One K piece of a leftover tile. Its partial sums go to the workspace in MFMA
+  // lane layout (one 16-B store per (wave, i, k, quarter, lane)); the workgroup
+  // whose piece completes the tile adds all pieces in piece order and runs the
+  // tile's epilogue. All pieces of a tile run on one XCD, whose L2 they share:
+  // each workgroup waits for its stores to be acknowledged by L2 before it counts
+  // itself in with one atomic, and nobody waits for anybody.
+  const int tt = piece / split;  // leftover tile within the XCD
+  const int tile_p = set_item(piece, true);
+  set_offsets(tile_p);
   prologue();
   wait_vm_lgkm0<0>();
 #pragma unroll
@@ -676,89 +686,88 @@ gemm_mfma_kernel(GemmArgs a) {
     if constexpr (ST > 2) step(std::integral_constant<int, 2 % ST>{}, k0 + 2);
     if constexpr (ST > 3) step(std::integral_constant<int, 3 % ST>{}, k0 + 3);
   }
-  float* wp = a.ws + (long)(xcd * per_xcd + piece) * (BM * BN);
+  using E = typename Op::elem_t;
+  auto part_off = [&](int i, int k, int q) {
+    return (((((long)wave * C::RN + i) * C::RM + k) * 4 + q) * 64 + lane) * 4;
+  };
+  {
+    float* wp = a.ws + kSplitCounters + (long)(xcd * per_xcd + piece) * (BM * BN);
+#pragma unroll
+    for (int i = 0; i < C::RN; ++i)
+#pragma unroll
+      for (int k = 0; k < C::RM; ++k)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          // copy the elements out first: a bit_cast of a vector-element expression reads element 0
+          const E e0 = acc[i][k][4 * q], e1 = acc[i][k][4 * q + 1], e2 = acc[i][k][4 * q + 2],
+                  e3 = acc[i][k][4 * q + 3];
+          *reinterpret_cast<float4*>(wp + part_off(i, k, q)) =
+              make_float4(__builtin_bit_cast(float, e0), __builtin_bit_cast(float, e1),
+                          __builtin_bit_cast(float, e2), __builtin_bit_cast(float, e3));
+        }
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's partial sums are in L2
+  __syncthreads();                                   // ... and every wave's; LDS reads done too
+  unsigned* cnt = reinterpret_cast<unsigned*>(a.ws) + xcd * per_xcd + tt;
+  if (tid == 0) s_flag = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                         (unsigned)(split - 1);
+  __syncthreads();
+  if (!s_flag) return;  // uniform
+  asm volatile("" ::: "memory");
+  if (tid == 0) *cnt = 0u;  // ready for the next launch
+  // Last piece in: sum the pieces in piece order, ((p0 + p1) + p2) + ..., the
+  // same sum whichever piece arrives last. This workgroup's own piece stays in
+  // registers; per 16-value block the pieces before it are added first, then it,
+  // then the pieces after it.
+  const int own = piece % split;
+  const float* wbase = a.ws + kSplitCounters + (long)(xcd * per_xcd + tt * split) * (BM * BN);
+  auto load_block = [&](int kc, int i, int k, E (&x)[16]) {
+    const float* wp = wbase + (long)kc * (BM * BN);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const float4 v = *reinterpret_cast<const float4*>(wp + part_off(i, k, q));
+      x[4 * q] = __builtin_bit_cast(E, v.x);
+      x[4 * q + 1] = __builtin_bit_cast(E, v.y);
+      x[4 * q + 2] = __builtin_bit_cast(E, v.z);
+      x[4 * q + 3] = __builtin_bit_cast(E, v.w);
+    }
+  };
 #pragma unroll
   for (int i = 0; i < C::RN; ++i)
 #pragma unroll
-    for (int k = 0; k < C::RM; ++k)
+    for (int k = 0; k < C::RM; ++k) {
+      if (own > 0) {
+        E t[16], x[16];
+        load_block(0, i, k, t);
+        for (int kc = 1; kc < own; ++kc) {
+          load_block(kc, i, k, x);
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const long e = ((((long)wave * C::RN + i) * C::RM + k) * 4 + q) * 64 + lane;
-        // copy the elements out first: a bit_cast of a vector-element expression reads element 0
-        using E = typename Op::elem_t;
-        const E e0 = acc[i][k][4 * q], e1 = acc[i][k][4 * q + 1], e2 = acc[i][k][4 * q + 2],
-                e3 = acc[i][k][4 * q + 3];
-        *reinterpret_cast<float4*>(wp + e * 4) =
-            make_float4(__builtin_bit_cast(float, e0), __builtin_bit_cast(float, e1), __builtin_bit_cast(float, e2),
-                        __builtin_bit_cast(float, e3));
+          for (int v = 0; v < 16; ++v) t[v] = t[v] + x[v];
+        }
+#pragma unroll
+        for (int v = 0; v < 16; ++v) acc[i][k][v] = t[v] + acc[i][k][v];
       }
-}
-
-// Second half of the K-split: one single-wave workgroup per (split tile, wave
-// sub-tile) of the GEMM's tile walk, so all CUs share the reduction. It adds the
-// pieces' partial sums in piece order and runs that wave's part of the tile
-// epilogue with the same code as the GEMM kernel. Grid: 8 * per_xcd * NW.
-template <class C, class Op, int EPI>
-__global__ void __launch_bounds__(64)
-gemm_split_reduce_kernel(GemmArgs a, int per_xcd) {
-  constexpr int BM = C::BM, BN = C::BN, BK = C::BK;
-  __shared__ __attribute__((aligned(1024))) uint16_t stage_buf[Staged<C, EPI>::value ? 32 * C::WTN : 8];
-  const int M = a.M_dev ? *a.M_dev : a.M;
-  const int tiles_m = (M + BM - 1) / BM, tiles_n = a.N / BN;
-  const int total = tiles_m * tiles_n;
-  const int nxcd = 8, xcd = blockIdx.x % nxcd, r = blockIdx.x / nxcd;
-  const int slot = r / C::NW, wave = r % C::NW;
-  const int chunk = (total + nxcd - 1) / nxcd;
-  int chunk_x = total - xcd * chunk;
-  chunk_x = chunk_x < 0 ? 0 : (chunk_x > chunk ? chunk : chunk_x);
-  int full_x, split;
-  split_plan(chunk_x, per_xcd, a.K / BK, full_x, split);
-  if (split < 2 || slot >= chunk_x - full_x) return;  // uniform
-  const int tile = xcd * chunk + full_x + slot;
-  const int gn = tiles_n < 8 ? tiles_n : 8;
-  const int GM = per_xcd / gn > 1 ? per_xcd / gn : 1;
-  const int gsz = GM * tiles_n;
-  const int g = tile / gsz, w = tile - g * gsz, gm0 = g * GM;
-  const int rows = tiles_m - gm0 < GM ? tiles_m - gm0 : GM;
-  const int m0 = (gm0 + w % rows) * BM, n0 = (w / rows) * BN;
-
-  const int lane = threadIdx.x;
-  const int wm = wave / C::WN, wn = wave % C::WN;
-  const int l32 = lane & 31, hi = lane >> 5;
-  using E = typename Op::elem_t;
-  typename Op::acc_t acc[C::RN][C::RM];
-  for (int kc = 0; kc < split; ++kc) {
-    const float* wp = a.ws + (long)(xcd * per_xcd + slot * split + kc) * (BM * BN);
-    float4 v[C::RN][C::RM][4];
+      for (int kc = own + 1; kc < split; ++kc) {
+        E x[16];
+        load_block(kc, i, k, x);
 #pragma unroll
-    for (int i = 0; i < C::RN; ++i)
-#pragma unroll
-      for (int k = 0; k < C::RM; ++k)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const long e = ((((long)wave * C::RN + i) * C::RM + k) * 4 + q) * 64 + lane;
-          v[i][k][q] = *reinterpret_cast<const float4*>(wp + e * 4);
-        }
-#pragma unroll
-    for (int i = 0; i < C::RN; ++i)
-#pragma unroll
-      for (int k = 0; k < C::RM; ++k)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const float f[4] = {v[i][k][q].x, v[i][k][q].y, v[i][k][q].z, v[i][k][q].w};
-#pragma unroll
-          for (int t = 0; t < 4; ++t) {
-            const E x = __builtin_bit_cast(E, f[t]);
-            acc[i][k][4 * q + t] = kc == 0 ? x : acc[i][k][4 * q + t] + x;
-          }
-        }
-  }
-  if constexpr (Staged<C, EPI>::value) {
-    StagedOperands<C, EPI> sop;
-    staged_preload<C, EPI>(a, sop, m0, n0, M, wm, wn, l32, hi);
-    staged_epilogue<C, EPI>(a, acc, sop, m0, n0, M, wm, wn, lane, l32, hi, stage_buf);
-  } else {
-    run_epilogue<C, EPI>(a, acc, m0, n0, M, wm, wn, l32, hi);
+        for (int v = 0; v < 16; ++v) acc[i][k][v] = acc[i][k][v] + x[v];
+      }
+    }
+  {
+    int m0, n0;
+    tile_mn(tile_p, m0, n0);
+    if constexpr (Staged<C, EPI>::value) {
+      StagedOperands<C, EPI> sop;
+      staged_preload<C, EPI>(a, sop, m0, n0, M, wm, wn, l32, hi);
+      constexpr int fs = ST - 1;
+      uint16_t* region = (wave < C::NW / 2 ? stA(std::integral_constant<int, fs>{})
+                                           : stB(std::integral_constant<int, fs>{})) +
+                         (wave % (C::NW / 2)) * 32 * C::WTN;
+      staged_epilogue<C, EPI>(a, acc, sop, m0, n0, M, wm, wn, lane, l32, hi, region);
+    } else {
+      run_epilogue<C, EPI>(a, acc, m0, n0, M, wm, wn, l32, hi);
+    }
   }
 }
 
@@ -783,18 +792,11 @@ hipError_t launch(const GemmArgs& a_in, hipStream_t s) {
   if (tiles_upper < grid) grid = ((tiles_upper + 7) / 8) * 8;
   if (grid < 8) grid = 8;
   GemmArgs a = a_in;
-  // the K-split needs a workspace slot per workgroup; QKV keeps whole tiles
-  if (a.ws && (EPI == EPI_QKV || a.ws_elems < grid * C::BM * C::BN)) a.ws = nullptr;
+  // the K-split needs the counters and a partial-sum tile per workgroup; QKV keeps whole tiles
+  if (a.ws && (EPI == EPI_QKV || grid > kSplitCounters || a.ws_elems < kSplitCounters + grid * C::BM * C::BN))
+    a.ws = nullptr;
   dfh_launch(kern, dim3((unsigned)grid), dim3(C::THREADS), 0, s, a);
-  hipError_t e = hipGetLastError();
-  if constexpr (EPI == EPI_QKV) {
-    return e;
-  } else {
-    if (e != hipSuccess || !a.ws) return e;
-    dfh_launch_aux(gemm_split_reduce_kernel<C, Op, EPI>, dim3((unsigned)(grid * C::NW)), dim3(64), 0, s, a,
-                   (int)(grid / 8));
-    return hipGetLastError();
-  }
+  return hipGetLastError();
 }
 
 // tile configurations: (BM, BN, BK, stages, wave grid)

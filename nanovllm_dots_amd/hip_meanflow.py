@@ -231,8 +231,7 @@ class HipFMHead:
     def profile(self, enable: bool) -> None:
         _lib.check(self.lib.dfh_profile_enable(self.handle, int(enable)), "dfh_profile_enable")
 
-    PROFILE_CLASSES = ("qkv_gemm", "o_gemm", "fc1_gemm", "fc2_gemm", "attention", "ln_modulate", "other",
-                       "o_gemm_splitk", "fc1_gemm_splitk", "fc2_gemm_splitk")
+    PROFILE_CLASSES = ("qkv_gemm", "o_gemm", "fc1_gemm", "fc2_gemm", "attention", "ln_modulate", "other")
 
     def profile_read(self) -> dict[str, tuple[float, int]]:
         k = len(self.PROFILE_CLASSES)

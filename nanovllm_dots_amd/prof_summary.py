@@ -11,7 +11,7 @@ calibrates both counters against the device copy of known size that
 dispatch: it reads and writes ``calib-mib`` MiB), and reports HBM bytes per
 dispatch per role. Roles follow dispatch order within a block: the gate-residual
 GEMM that follows attention is the O projection, the one that follows the
-GELU GEMM is fc2; a K-split reduction kernel takes its GEMM's role + ``_splitk``.
+GELU GEMM is fc2.
 """
 from __future__ import annotations
 
@@ -37,10 +37,6 @@ def roles(names):
     prev = ""
     for n in names:
         s = short_name(n)
-        if s.startswith("gemm_split_reduce_kernel"):
-            # the K-split reduction of the GEMM just before it
-            out.append(prev + "_splitk" if prev.endswith("_gemm") else "gemm_splitk")
-            continue
         m = _EPI.search(s) if s.startswith("gemm_mfma_kernel") else None
         if m:
             epi = int(m.group(1))
@@ -95,8 +91,8 @@ def pmc(fetch_csv: str, write_csv: str, calib_mib: int):
     return factors, out
 
 
-def pmc_table(factors, out, roles_wanted=("qkv_gemm", "o_gemm", "fc1_gemm", "fc1_gemm_splitk", "fc2_gemm",
-                                          "fc2_gemm_splitk", "attention", "ln_modulate")) -> str:
+def pmc_table(factors, out, roles_wanted=("qkv_gemm", "o_gemm", "fc1_gemm", "fc2_gemm", "attention",
+                                          "ln_modulate")) -> str:
     lines = ["| role | dispatches | FETCH_SIZE KiB (raw median) | WRITE_SIZE KiB (raw median) | "
              "HBM read MB | HBM write MB | HBM total MB |", "|---|---:|---:|---:|---:|---:|---:|"]
     machine = []

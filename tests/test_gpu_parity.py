@@ -263,7 +263,7 @@ def test_gemm_ksplit_matches_whole_tiles(M, K, N, tile, epi):
     B = (0.02 * torch.randn(N, K, generator=g)).bfloat16().cuda()
     bias = (0.1 * torch.randn(N, generator=g)).bfloat16().cuda()
     dt = torch.float32 if epi == 4 else torch.bfloat16
-    ws = torch.empty(1 << 26, dtype=torch.uint8, device="cuda")
+    ws = torch.zeros((1 << 26) + (1 << 16), dtype=torch.uint8, device="cuda")  # zero-filled before first use
     outs = []
     for use_ws in (False, True):
         C = torch.zeros((M, N), device="cuda", dtype=dt)

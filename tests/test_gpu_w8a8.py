@@ -130,7 +130,8 @@ def test_quantize_dit_swaps_eligible_linears():
 
 
 def _split_ws():
-    return torch.empty(1 << 26, dtype=torch.uint8, device="cuda")  # 64 MiB: one 256x256 f32 tile per CU
+    # one 256x256 f32 partial tile + one counter per CU (256 CUs); zero-filled before first use
+    return torch.zeros((1 << 26) + (1 << 16), dtype=torch.uint8, device="cuda")
 
 
 @pytest.mark.parametrize("M,K,N,tile", [(36937, 4096, 1024, 0), (36937, 1024, 4096, 0), (3000, 2048, 256, 3)])
