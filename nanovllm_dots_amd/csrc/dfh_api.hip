@@ -146,16 +146,17 @@ hipError_t gemm(DfhHandle* h, int pc, const GemmArgs& a_in, int epi, hipStream_t
 }
 
 // Tile shape per GEMM role (indices of gemm_bf16's configurations), chosen from
-// measured throughput at M ~ 37k rows: 8-wave 256x256 for the wide (N=4096) and the
-// deep (K=4096) products, two 128x128 workgroups per CU for N=1024, K=1024 (their
+// measured throughput at M ~ 37k rows: 8-wave 256x256 tiles whose K-step DMA is
+// issued by one half of the workgroup for the fused QKV, the wide (N=4096) and the
+// deep (K=4096) products; two 128x128 workgroups per CU for N=1024, K=1024 (their
 // epilogues overlap the other workgroup's MFMAs; 256-wide tiles would leave a third
-// of the last round idle) and for the fused QKV.
+// of the last round idle).
 enum GemmRole { kRoleQKV, kRoleNarrow, kRoleWide };
 int tile_for(long M, int N, int K, GemmRole role) {
   if (M < 4096) return -1;  // small problems: the library heuristic
-  if (role == kRoleQKV) return 2;
-  if (role == kRoleWide) return N % 256 == 0 ? 0 : -1;
-  if (K >= 4096 && N % 256 == 0) return 0;
+  if (role == kRoleQKV) return N % 256 == 0 ? 8 : 2;
+  if (role == kRoleWide) return N % 256 == 0 ? 8 : -1;
+  if (K >= 4096 && N % 256 == 0) return 8;
   // narrow outputs (N = hidden) at K = hidden: 128x128 tiles, two workgroups per
   // CU; 256-wide tiles (N/256 column blocks) leave up to a third of the last round idle
   return (N % 128 == 0 && K % 64 == 0) ? 2 : -1;

@@ -27,9 +27,18 @@ namespace dfh {
 namespace {
 
 
-template <int BM_, int BN_, int BK_, int ST_, int WM_, int WN_>
+// K-loop schedules (per K step: wait for this wave's DMA of step k, barrier,
+// DMA of step k+ST-1, fragment reads and MFMAs):
+//  SCHED 0: every wave issues its share of the DMA.
+//  SCHED 1: the DMA of step j is issued by one half of the workgroup (waves
+//           4(j%2) .. 4(j%2)+3). The vector-memory path takes ~16 cycles per
+//           1 KB DMA instruction, so a step's 64 instructions queue for ~1000
+//           cycles and hold up the MFMAs of every wave that issued one; the half
+//           that issues none starts its MFMAs right after the barrier.
+template <int BM_, int BN_, int BK_, int ST_, int WM_, int WN_, int SCHED_ = 0>
 struct Cfg {
-  static constexpr int BM = BM_, BN = BN_, BK = BK_, ST = ST_, WM = WM_, WN = WN_;
+  static constexpr int BM = BM_, BN = BN_, BK = BK_, ST = ST_, WM = WM_, WN = WN_, SCHED = SCHED_;
+  static constexpr int HD = SCHED == 1;  // the DMA of step j issued by half j % 2
   static constexpr int THREADS = 64 * WM * WN;
   static constexpr int NW = WM * WN;
   static constexpr int WTM = BM / WM;  // wave tile rows (activations)
@@ -38,7 +47,8 @@ struct Cfg {
   static constexpr int RN = WTN / 32;
   static constexpr int CH = BK / 8;                 // 16-B chunks per LDS row
   static constexpr int ROWS_PER_DMA = 64 / CH;      // rows one wave fills per DMA (1 KB)
-  static constexpr int RPR = NW * ROWS_PER_DMA;     // rows per DMA round of the workgroup
+  static constexpr int DW = HD ? NW / 2 : NW;       // waves that issue one step's DMA
+  static constexpr int RPR = DW * ROWS_PER_DMA;     // rows per DMA round of the workgroup
   static constexpr int AJ = BM / RPR, BJ = BN / RPR;
   static constexpr int LPS = AJ + BJ;               // DMA instructions per wave per K step
   static constexpr int LDS_BYTES = ST * (BM + BN) * BK * 2;
@@ -49,6 +59,7 @@ struct Cfg {
   static_assert(BM % RPR == 0 && BN % RPR == 0, "DMA rounds");
   static_assert(BK == 32 || BK == 64, "BK");
   static_assert(ST >= 1 && ST <= 4, "stages");
+  static_assert(!HD || NW == 8, "half DMA: 8 waves");
 };
 
 // LDS tile layout: rows of BK bf16 (BK/8 16-B chunks), row-major, logical chunk
@@ -463,7 +474,7 @@ gemm_mfma_kernel(GemmArgs a) {
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: LDS / DMA bases in SGPRs
   const int wm = wave / C::WN, wn = wave % C::WN;
   const int l32 = lane & 31, hi = lane >> 5;
 
@@ -500,7 +511,8 @@ gemm_mfma_kernel(GemmArgs a) {
   // resource's range and arrive as zeros, so no row clamping; per lane only one
   // 32-bit byte offset per operand stays live.
   static_assert(C::RPR % 16 == 0, "swizzle must not depend on the DMA round");
-  const int dma_row = wave * C::ROWS_PER_DMA + lane / CH;
+  const int dma_wave = wave % C::DW;
+  const int dma_row = dma_wave * C::ROWS_PER_DMA + lane / CH;
   const uint32_t dma_col = (uint32_t)(((lane % CH) ^ swz<CH>(dma_row)) << 3);
   const uint32_t va = ((uint32_t)dma_row * (uint32_t)a.lda + dma_col) * 2u;
   const uint32_t vb = ((uint32_t)dma_row * (uint32_t)a.ldb + dma_col) * 2u;
@@ -516,6 +528,7 @@ gemm_mfma_kernel(GemmArgs a) {
                                            (int)((uint32_t)BN * (uint32_t)a.ldb * 2u), kBufferFlags);
   };
   auto dma = [&](auto stc, int kstep) {
+    if (C::HD && (wave >> 2) != (kstep & 1)) return;  // uniform per wave
     uint16_t* la = stA(stc);
     uint16_t* lb = stB(stc);
     const int koff = kstep * BK * 2;
@@ -524,16 +537,16 @@ gemm_mfma_kernel(GemmArgs a) {
     uint32_t vo = va;
 #pragma unroll
     for (int j = 0; j < C::AJ; ++j) {
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, DFH_LPTR(la + (j * C::RPR + wave * C::ROWS_PER_DMA) * BK), 16,
-                                               vo, koff, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, DFH_LPTR(la + (j * C::RPR + dma_wave * C::ROWS_PER_DMA) * BK),
+                                               16, vo, koff, 0, 0);
       vo += a_round;
       asm volatile("" : "+v"(vo));
     }
     vo = vb;
 #pragma unroll
     for (int j = 0; j < C::BJ; ++j) {
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, DFH_LPTR(lb + (j * C::RPR + wave * C::ROWS_PER_DMA) * BK), 16,
-                                               vo, koff, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, DFH_LPTR(lb + (j * C::RPR + dma_wave * C::ROWS_PER_DMA) * BK),
+                                               16, vo, koff, 0, 0);
       vo += b_round;
       asm volatile("" : "+v"(vo));
     }
@@ -600,7 +613,15 @@ gemm_mfma_kernel(GemmArgs a) {
     if (k + ST - 1 < KTi) dma(std::integral_constant<int, (s + ST - 1) % ST>{}, kb + k + ST - 1);
     compute(stc);
   };
-  auto prologue = [&]() {
+  auto kloop = [&]() __attribute__((always_inline)) {
+    for (int k0 = 0; k0 < KTi; k0 += ST) {
+      step(std::integral_constant<int, 0>{}, k0);
+      if constexpr (ST > 1) step(std::integral_constant<int, 1 % ST>{}, k0 + 1);
+      if constexpr (ST > 2) step(std::integral_constant<int, 2 % ST>{}, k0 + 2);
+      if constexpr (ST > 3) step(std::integral_constant<int, 3 % ST>{}, k0 + 3);
+    }
+  };
+  auto prologue = [&]() __attribute__((always_inline)) {
     dma(std::integral_constant<int, 0>{}, kb);
     if constexpr (ST > 2) { if (1 < KTi) dma(std::integral_constant<int, 1 % ST>{}, kb + 1); }
     if constexpr (ST > 3) { if (2 < KTi) dma(std::integral_constant<int, 2 % ST>{}, kb + 2); }
@@ -632,12 +653,7 @@ gemm_mfma_kernel(GemmArgs a) {
       for (int k = 0; k < C::RM; ++k)
 #pragma unroll
         for (int t = 0; t < 16; ++t) acc[i][k][t] = 0;
-    for (int k0 = 0; k0 < KT; k0 += ST) {
-      step(std::integral_constant<int, 0>{}, k0);
-      if constexpr (ST > 1) step(std::integral_constant<int, 1 % ST>{}, k0 + 1);
-      if constexpr (ST > 2) step(std::integral_constant<int, 2 % ST>{}, k0 + 2);
-      if constexpr (ST > 3) step(std::integral_constant<int, 3 % ST>{}, k0 + 3);
-    }
+    kloop();
     // every wave is done with every stage before it is refilled
     wait_vm_lgkm0<0>();
     __builtin_amdgcn_s_barrier();
@@ -680,12 +696,7 @@ gemm_mfma_kernel(GemmArgs a) {
     for (int k = 0; k < C::RM; ++k)
 #pragma unroll
       for (int t = 0; t < 16; ++t) acc[i][k][t] = 0;
-  for (int k0 = 0; k0 < KTi; k0 += ST) {
-    step(std::integral_constant<int, 0>{}, k0);
-    if constexpr (ST > 1) step(std::integral_constant<int, 1 % ST>{}, k0 + 1);
-    if constexpr (ST > 2) step(std::integral_constant<int, 2 % ST>{}, k0 + 2);
-    if constexpr (ST > 3) step(std::integral_constant<int, 3 % ST>{}, k0 + 3);
-  }
+  kloop();
   using E = typename Op::elem_t;
   auto part_off = [&](int i, int k, int q) {
     return (((((long)wave * C::RN + i) * C::RM + k) * 4 + q) * 64 + lane) * 4;
@@ -808,11 +819,13 @@ using T4 = Cfg<256, 128, 64, 2, 2, 2>;  // 4 waves, 128x64 per wave, 96 KB
 using T5 = Cfg<128, 256, 32, 3, 2, 2>;  // 4 waves, 64x128 per wave, 72 KB: two per CU
 using T6 = Cfg<256, 128, 64, 3, 2, 2>;  // 4 waves, 3 stages, 144 KB
 using T7 = Cfg<128, 128, 32, 4, 2, 2>;  // 4 waves, 4 stages of BK 32, 64 KB: two per CU
-constexpr int kNumTiles = 8;
-const int kTileBM[kNumTiles] = {T0::BM, T1::BM, T2::BM, T3::BM, T4::BM, T5::BM, T6::BM, T7::BM};
-const int kTileBN[kNumTiles] = {T0::BN, T1::BN, T2::BN, T3::BN, T4::BN, T5::BN, T6::BN, T7::BN};
-const int kTileBK[kNumTiles] = {T0::BK, T1::BK, T2::BK, T3::BK, T4::BK, T5::BK, T6::BK, T7::BK};
-const int kTileWTN[kNumTiles] = {T0::WTN, T1::WTN, T2::WTN, T3::WTN, T4::WTN, T5::WTN, T6::WTN, T7::WTN};
+using T8 = Cfg<256, 256, 64, 2, 2, 4, 1>;  // T0 with the DMA of a step issued by one half
+constexpr int kNumTiles = 9;
+const int kTileBM[kNumTiles] = {T0::BM, T1::BM, T2::BM, T3::BM, T4::BM, T5::BM, T6::BM, T7::BM, T8::BM};
+const int kTileBN[kNumTiles] = {T0::BN, T1::BN, T2::BN, T3::BN, T4::BN, T5::BN, T6::BN, T7::BN, T8::BN};
+const int kTileBK[kNumTiles] = {T0::BK, T1::BK, T2::BK, T3::BK, T4::BK, T5::BK, T6::BK, T7::BK, T8::BK};
+const int kTileWTN[kNumTiles] = {T0::WTN, T1::WTN, T2::WTN, T3::WTN, T4::WTN, T5::WTN, T6::WTN, T7::WTN,
+                                 T8::WTN};
 
 template <class Op, int EPI>
 hipError_t dispatch_tiles(const GemmArgs& a, hipStream_t s, int tile) {
@@ -825,6 +838,7 @@ hipError_t dispatch_tiles(const GemmArgs& a, hipStream_t s, int tile) {
     case 5: return launch<T5, Op, EPI>(a, s);
     case 6: return launch<T6, Op, EPI>(a, s);
     case 7: return launch<T7, Op, EPI>(a, s);
+    case 8: return launch<T8, Op, EPI>(a, s);
     default: return hipErrorInvalidValue;
   }
 }
@@ -832,7 +846,7 @@ hipError_t dispatch_tiles(const GemmArgs& a, hipStream_t s, int tile) {
 int pick_tile(const GemmArgs& a) {
   const long cus = num_cus();
   const long t0 = (long)((a.M + 255) / 256) * (a.N / 256);
-  if (a.N % 256 == 0 && a.K % 64 == 0 && t0 >= 2 * cus) return 0;
+  if (a.N % 256 == 0 && a.K % 64 == 0 && t0 >= 2 * cus) return 8;
   if (a.N % 128 == 0 && a.K % 64 == 0 && (long)((a.M + 127) / 128) * (a.N / 128) >= cus) return 2;
   return 3;
 }

@@ -53,7 +53,8 @@ GEMM_CASES = [(1, 64, 64, 3), (37, 128, 256, 2), (300, 1024, 1024, -1), (700, 10
               (1000, 3072, 1024, 1), (513, 1024, 4096, -1), (64, 75776 // 8, 1024, -1),
               (777, 512, 1024, 4), (1500, 4096, 1024, 0), (20, 256, 64, 0), (333, 256, 192, 1),
               (1111, 1024, 1024, 5), (600, 1024, 4096, 6), (259, 512, 1024, 7), (1234, 3072, 1024, 1),
-              (100, 512, 96, 7), (70, 256, 160, 5)]
+              (100, 512, 96, 7), (70, 256, 160, 5), (1500, 4096, 1024, 8), (3001, 1024, 4096, 8),
+              (20, 256, 64, 8)]
 
 
 @pytest.mark.parametrize("M,N,K,tile", GEMM_CASES)
@@ -251,8 +252,9 @@ def test_full_size_nfe4_solve():
     _assert_latents(got, ref, cfg.latent_dim, "full-nfe4")
 
 
-@pytest.mark.parametrize("M,K,N,tile,epi", [(36937, 4096, 1024, 0, 4), (36937, 1024, 4096, 0, 1),
-                                            (3000, 2048, 256, 3, 4), (700, 1024, 256, 3, 0)])
+@pytest.mark.parametrize("M,K,N,tile,epi", [(36937, 4096, 1024, 8, 4), (36937, 1024, 4096, 8, 1),
+                                            (20000, 1024, 4096, 0, 4), (3000, 2048, 256, 3, 4),
+                                            (700, 1024, 256, 3, 0)])
 def test_gemm_ksplit_matches_whole_tiles(M, K, N, tile, epi):
     """bf16 GEMM with the K-split workspace vs without (float32 sums in a
     different order: f32 output to 1e-5 relative, bf16 output to one ulp)."""
