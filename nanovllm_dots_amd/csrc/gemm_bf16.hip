@@ -108,14 +108,21 @@ struct OpI8 {
 // filling, then stores it back as whole rows, 16 B per lane (8 full 128-B rows
 // per store instruction instead of 32 partial rows). Needs NW * 32 * WTN bf16
 // of free stage: half the waves in the A buffer, half in the B buffer.
+// The gate-residual epilogue reads its residual and gate rows the same way,
+// 16 B per lane, one 32-row block ahead of the block it stores.
 template <class C, int EPI>
 struct Staged {
-  static constexpr bool kEpi = EPI == EPI_BIAS || EPI == EPI_GELU;
+  static constexpr bool kEpi = EPI == EPI_BIAS || EPI == EPI_GELU || EPI == EPI_GATE_RES;
   static constexpr int kSmall = C::BM < C::BN ? C::BM : C::BN;
   static constexpr bool value = kEpi && (C::NW / 2) * 32 * C::WTN <= kSmall * C::BK && C::NW % 2 == 0;
   static constexpr int CPR = C::WTN / 8;   // 16-B chunks per staged row
   static constexpr int RPI = 64 / CPR;     // rows per wave-wide 16-B access
-  static constexpr int kStores = C::RM * (32 / RPI);
+  static constexpr int JB = 32 / RPI;      // wave-wide accesses per 32-row block
+  static constexpr int kStores = C::RM * JB;
+  static constexpr bool kRes = EPI == EPI_GATE_RES;
+  // vector-memory ops the epilogue issues after the next tile's prologue DMA
+  // (stores, and the residual + gate loads of blocks 1 .. RM-1), on every path
+  static constexpr int kVmAfter = kStores + (kRes ? (C::RM - 1) * 2 * JB : 0);
 };
 
 // staged element offset: row r (0..31) of the block, 16-B chunk c, slot c ^ ((r >> 1) & 7)
@@ -129,14 +136,54 @@ __device__ __forceinline__ int stage_off(int r, int c) {
 // in issue order, so a later load would make its first use wait for that DMA.
 template <class C, int EPI>
 struct StagedOperands {
+  static constexpr int JB = Staged<C, EPI>::JB, NRES = Staged<C, EPI>::kRes ? JB : 1;
   float b[C::RN][4][4];
   float w[EPI == EPI_DQ ? C::RN : 1][4][4];
   float sx[EPI == EPI_DQ ? C::RM : 1];
+  uint4 x0[NRES], g0[NRES];  // gate-residual: residual and gate chunks of block 0
 };
 
+// Gate-residual rows a lane stores: row j*RPI + lane/CPR of each 32-row block,
+// columns (lane % CPR)*8 .. +8. Their requests (row -> request table) are read
+// at the start of the tile, so the gate address is known when the epilogue needs it.
 template <class C, int EPI>
-__device__ __forceinline__ void staged_preload(const GemmArgs& a, StagedOperands<C, EPI>& op, int m0, int n0,
-                                               int M, int wm, int wn, int l32, int hi) {
+struct ResRows {
+  int rq[Staged<C, EPI>::kRes ? C::RM * Staged<C, EPI>::JB : 1];
+};
+template <class C, int EPI>
+__device__ __forceinline__ void res_rows_load(const GemmArgs& a, ResRows<C, EPI>& rr, int m0, int M, int wm,
+                                              int lane) {
+  if constexpr (Staged<C, EPI>::kRes && Staged<C, EPI>::value) {
+    using S = Staged<C, EPI>;
+#pragma unroll
+    for (int k = 0; k < C::RM; ++k)
+#pragma unroll
+      for (int j = 0; j < S::JB; ++j) {
+        const int m = m0 + wm * C::WTM + k * 32 + j * S::RPI + lane / S::CPR;
+        rr.rq[k * S::JB + j] = a.row_req[m < M ? m : M - 1];
+      }
+  }
+}
+// residual and gate chunks of block k (rows clamped to M - 1: always issued)
+template <class C, int EPI>
+__device__ __forceinline__ void res_block_load(const GemmArgs& a, const ResRows<C, EPI>& rr, int k, int m0, int n0,
+                                               int M, int wm, int wn, int lane, uint4 (&x)[Staged<C, EPI>::JB],
+                                               uint4 (&g)[Staged<C, EPI>::JB]) {
+  using S = Staged<C, EPI>;
+  const int n = n0 + wn * C::WTN + (lane % S::CPR) * 8;
+#pragma unroll
+  for (int j = 0; j < S::JB; ++j) {
+    const int m = m0 + wm * C::WTM + k * 32 + j * S::RPI + lane / S::CPR;
+    const int mm = m < M ? m : M - 1;
+    x[j] = *reinterpret_cast<const uint4*>(a.C + (long)mm * a.ldc + n);
+    g[j] = *reinterpret_cast<const uint4*>(a.gate + (long)rr.rq[k * S::JB + j] * a.ld_gate + n);
+  }
+}
+
+template <class C, int EPI>
+__device__ __forceinline__ void staged_preload(const GemmArgs& a, StagedOperands<C, EPI>& op,
+                                               const ResRows<C, EPI>& rr, int m0, int n0, int M, int wm, int wn,
+                                               int lane, int l32, int hi) {
   // one uniform branch around all loads, so they issue back to back and are waited for once
   uint2 braw[C::RN][4];
   if (a.bias) {
@@ -169,17 +216,25 @@ __device__ __forceinline__ void staged_preload(const GemmArgs& a, StagedOperands
       op.sx[k] = a.sx[m < M ? m : M - 1];
     }
   }
+  if constexpr (Staged<C, EPI>::kRes) res_block_load<C, EPI>(a, rr, 0, m0, n0, M, wm, wn, lane, op.x0, op.g0);
 }
 
 template <class C, int EPI, class ACC>
 __device__ __forceinline__ void staged_epilogue(const GemmArgs& a, ACC (&acc)[C::RN][C::RM],
-                                                const StagedOperands<C, EPI>& op, int m0, int n0, int M,
-                                                int wm, int wn, int lane, int l32, int hi, uint16_t* region) {
+                                                const StagedOperands<C, EPI>& op, const ResRows<C, EPI>& rr,
+                                                int m0, int n0, int M, int wm, int wn, int lane, int l32, int hi,
+                                                uint16_t* region) {
   using S = Staged<C, EPI>;
-  constexpr int CPR = S::CPR, RPI = S::RPI;
+  constexpr int CPR = S::CPR, RPI = S::RPI, JB = S::JB, NB = S::kRes ? 2 : 1, NJ = S::kRes ? JB : 1;
   const __amdgpu_buffer_rsrc_t rc = __builtin_amdgcn_make_buffer_rsrc(
       (void*)(a.C + (long)m0 * a.ldc), (short)0, (int)((uint32_t)(M - m0) * (uint32_t)a.ldc * 2u), kBufferFlags);
   const int ncol0 = n0 + wn * C::WTN;
+  // gate-residual: residual / gate chunks, double-buffered by block
+  uint4 xb[NB][NJ], gb[NB][NJ];
+  if constexpr (S::kRes) {
+#pragma unroll
+    for (int j = 0; j < JB; ++j) { xb[0][j] = op.x0[j]; gb[0][j] = op.g0[j]; }
+  }
 #pragma unroll
   for (int k = 0; k < C::RM; ++k) {
     // MFMA layout -> LDS: lane (l32, hi) holds row l32, columns i*32 + 8g + 4hi + [0, 4)
@@ -203,12 +258,33 @@ __device__ __forceinline__ void staged_epilogue(const GemmArgs& a, ACC (&acc)[C:
         }
         *reinterpret_cast<uint2*>(region + stage_off<CPR>(l32, 4 * i + g) + 4 * hi) = pack4(y[0], y[1], y[2], y[3]);
       }
+    // the next block's residual / gate reads go out before this block's stores,
+    // so waiting for them later never waits for these stores
+    if constexpr (S::kRes) {
+      if (k + 1 < C::RM) res_block_load<C, EPI>(a, rr, k + 1, m0, n0, M, wm, wn, lane, xb[(k + 1) & 1], gb[(k + 1) & 1]);
+    }
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     // LDS -> rows: lane reads 16 B of row j*RPI + lane/CPR and stores it
 #pragma unroll
-    for (int j = 0; j < 32 / RPI; ++j) {
+    for (int j = 0; j < JB; ++j) {
       const int r = j * RPI + lane / CPR, c = lane % CPR;
-      const uint4 v = *reinterpret_cast<const uint4*>(region + stage_off<CPR>(r, c));
+      uint4 v = *reinterpret_cast<const uint4*>(region + stage_off<CPR>(r, c));
+      if constexpr (S::kRes) {
+        // out = x + bf16(gate * bf16(y)), y = acc + bias already rounded to bf16 in LDS
+        float yv[8], xv[8], gv[8];
+        unpack4(make_uint2(v.x, v.y), yv);
+        unpack4(make_uint2(v.z, v.w), yv + 4);
+        const uint4 xq = xb[k & 1][j], gq = gb[k & 1][j];
+        unpack4(make_uint2(xq.x, xq.y), xv);
+        unpack4(make_uint2(xq.z, xq.w), xv + 4);
+        unpack4(make_uint2(gq.x, gq.y), gv);
+        unpack4(make_uint2(gq.z, gq.w), gv + 4);
+        float o[8];
+#pragma unroll
+        for (int t = 0; t < 8; ++t) o[t] = xv[t] + rbf(gv[t] * yv[t]);
+        const uint2 lo = pack4(o[0], o[1], o[2], o[3]), hi2 = pack4(o[4], o[5], o[6], o[7]);
+        v = make_uint4(lo.x, lo.y, hi2.x, hi2.y);
+      }
       const int rt = wm * C::WTM + k * 32 + r;  // row within the tile
       const int n = ncol0 + c * 8;
       const u32x4 o = {v.x, v.y, v.z, v.w};
@@ -583,7 +659,7 @@ gemm_mfma_kernel(GemmArgs a) {
   // tile's first step waits for vmcnt <= kEpiStores (+ the later prologue
   // stages) and leaves the stores in flight. The QKV epilogue (data-dependent
   // store count) waits for zero.
-  constexpr int kEpiStoresRaw = (EPI == EPI_QKV) ? -1 : Staged<C, EPI>::value ? Staged<C, EPI>::kStores
+  constexpr int kEpiStoresRaw = (EPI == EPI_QKV) ? -1 : Staged<C, EPI>::value ? Staged<C, EPI>::kVmAfter
                                                                              : C::RN * C::RM * 4;
   constexpr int kWaitBase = ST >= 2 ? (ST - 2) * C::LPS : 0;
   // vmcnt holds at most 63: larger counts fall back to a full wait
@@ -653,12 +729,14 @@ gemm_mfma_kernel(GemmArgs a) {
       for (int k = 0; k < C::RM; ++k)
 #pragma unroll
         for (int t = 0; t < 16; ++t) acc[i][k][t] = 0;
+    ResRows<C, EPI> rrows;
+    res_rows_load<C, EPI>(a, rrows, m0, M, wm, lane);  // lands during the K loop
     kloop();
     // every wave is done with every stage before it is refilled
     wait_vm_lgkm0<0>();
     __builtin_amdgcn_s_barrier();
     StagedOperands<C, EPI> sop;
-    if constexpr (Staged<C, EPI>::value) staged_preload<C, EPI>(a, sop, m0, n0, M, wm, wn, l32, hi);
+    if constexpr (Staged<C, EPI>::value) staged_preload<C, EPI>(a, sop, rrows, m0, n0, M, wm, wn, lane, l32, hi);
     // start the next tile's first K steps under this tile's epilogue
     jt += per_xcd;
     const int next = tile_at(jt);
@@ -672,7 +750,7 @@ gemm_mfma_kernel(GemmArgs a) {
       uint16_t* region = (wave < C::NW / 2 ? stA(std::integral_constant<int, fs>{})
                                            : stB(std::integral_constant<int, fs>{})) +
                          (wave % (C::NW / 2)) * 32 * C::WTN;
-      staged_epilogue<C, EPI>(a, acc, sop, m0, n0, M, wm, wn, lane, l32, hi, region);
+      staged_epilogue<C, EPI>(a, acc, sop, rrows, m0, n0, M, wm, wn, lane, l32, hi, region);
     } else {
       run_epilogue<C, EPI>(a, acc, m0, n0, M, wm, wn, l32, hi);
     }
@@ -770,12 +848,14 @@ gemm_mfma_kernel(GemmArgs a) {
     tile_mn(tile_p, m0, n0);
     if constexpr (Staged<C, EPI>::value) {
       StagedOperands<C, EPI> sop;
-      staged_preload<C, EPI>(a, sop, m0, n0, M, wm, wn, l32, hi);
+      ResRows<C, EPI> rrows;
+      res_rows_load<C, EPI>(a, rrows, m0, M, wm, lane);
+      staged_preload<C, EPI>(a, sop, rrows, m0, n0, M, wm, wn, lane, l32, hi);
       constexpr int fs = ST - 1;
       uint16_t* region = (wave < C::NW / 2 ? stA(std::integral_constant<int, fs>{})
                                            : stB(std::integral_constant<int, fs>{})) +
                          (wave % (C::NW / 2)) * 32 * C::WTN;
-      staged_epilogue<C, EPI>(a, acc, sop, m0, n0, M, wm, wn, lane, l32, hi, region);
+      staged_epilogue<C, EPI>(a, acc, sop, rrows, m0, n0, M, wm, wn, lane, l32, hi, region);
     } else {
       run_epilogue<C, EPI>(a, acc, m0, n0, M, wm, wn, l32, hi);
     }
