@@ -631,25 +631,36 @@ gemm_mfma_kernel(GemmArgs a) {
   const int fa_row = wm * C::WTM + l32;
   const int fb_row = wn * C::WTN + l32;
   typename Op::acc_t acc[C::RN][C::RM];
+  // Fragments are double-buffered across the 16-deep k slices: the reads of
+  // slice kk+1 are issued before the MFMAs of slice kk, so a wave running alone
+  // on its SIMD has its next operands in flight while its MFMAs execute.
   auto compute = [&](auto stc) {
     const uint16_t* la = stA(stc);
     const uint16_t* lb = stB(stc);
-#pragma unroll
-    for (int kk = 0; kk < BK / 16; ++kk) {
+    bf16x8 fa[2][C::RM], fb[2][C::RN];
+    auto read = [&](int kk, bf16x8 (&ra)[C::RM], bf16x8 (&rb)[C::RN]) {
       const int ch = 2 * kk + hi;
-      bf16x8 fa[C::RM], fb[C::RN];
 #pragma unroll
       for (int i = 0; i < C::RM; ++i)
-        fa[i] = *reinterpret_cast<const bf16x8*>(la + lds_off<CH>(fa_row + i * 32, ch));
+        ra[i] = *reinterpret_cast<const bf16x8*>(la + lds_off<CH>(fa_row + i * 32, ch));
 #pragma unroll
       for (int i = 0; i < C::RN; ++i)
-        fb[i] = *reinterpret_cast<const bf16x8*>(lb + lds_off<CH>(fb_row + i * 32, ch));
+        rb[i] = *reinterpret_cast<const bf16x8*>(lb + lds_off<CH>(fb_row + i * 32, ch));
+    };
+    read(0, fa[0], fb[0]);
+#pragma unroll
+    for (int kk = 0; kk < BK / 16; ++kk) {
+      // the fences keep the compiler from sinking the reads back to their uses
+      __builtin_amdgcn_sched_barrier(0);
+      if (kk + 1 < BK / 16) read(kk + 1, fa[(kk + 1) & 1], fb[(kk + 1) & 1]);
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int i = 0; i < C::RN; ++i)
 #pragma unroll
         for (int k = 0; k < C::RM; ++k)
-          acc[i][k] = Op::mma(fb[i], fa[k], acc[i][k]);
+          acc[i][k] = Op::mma(fb[kk & 1][i], fa[kk & 1][k], acc[i][k]);
     }
+    __builtin_amdgcn_sched_barrier(0);
   };
 
   const int KT = K / BK;
