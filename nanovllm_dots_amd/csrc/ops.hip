@@ -18,6 +18,9 @@ ln_modulate_kernel(const uint16_t* __restrict__ x, long ldx, uint16_t* __restric
                    const uint16_t* __restrict__ shift, const uint16_t* __restrict__ scale,
                    long ld_mod, const int* __restrict__ row_req, const int* __restrict__ row_map,
                    int rows, const int* __restrict__ M_dev, int H, float eps) {
+  // 16-B accesses (8 values) where the row splits evenly, else 8-B
+  constexpr int W = VPT % 8 == 0 ? 8 : 4;
+  constexpr int NJ = VPT / W;
   const int lane = threadIdx.x & 63;
   const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
   const int nrows = M_dev ? *M_dev : rows;
@@ -25,11 +28,28 @@ ln_modulate_kernel(const uint16_t* __restrict__ x, long ldx, uint16_t* __restric
   const int src = row_map ? row_map[r] : r;
   const int req = row_req[src];
   const uint16_t* xp = x + (long)src * ldx;
-  float v[VPT];
+  const uint16_t* shp = shift + (long)req * ld_mod;
+  const uint16_t* scp = scale + (long)req * ld_mod;
+  // the row and its request's shift / scale all in flight before the reductions
+  float v[VPT], sh[VPT], sc[VPT];
 #pragma unroll
-  for (int j = 0; j < VPT / 4; ++j) {
-    const int col = (j * 64 + lane) * 4;
-    unpack4(*reinterpret_cast<const uint2*>(xp + col), v + 4 * j);
+  for (int j = 0; j < NJ; ++j) {
+    const int col = (j * 64 + lane) * W;
+    if constexpr (W == 8) {
+      const uint4 xq = *reinterpret_cast<const uint4*>(xp + col);
+      const uint4 hq = *reinterpret_cast<const uint4*>(shp + col);
+      const uint4 cq = *reinterpret_cast<const uint4*>(scp + col);
+      unpack4(make_uint2(xq.x, xq.y), v + 8 * j);
+      unpack4(make_uint2(xq.z, xq.w), v + 8 * j + 4);
+      unpack4(make_uint2(hq.x, hq.y), sh + 8 * j);
+      unpack4(make_uint2(hq.z, hq.w), sh + 8 * j + 4);
+      unpack4(make_uint2(cq.x, cq.y), sc + 8 * j);
+      unpack4(make_uint2(cq.z, cq.w), sc + 8 * j + 4);
+    } else {
+      unpack4(*reinterpret_cast<const uint2*>(xp + col), v + 4 * j);
+      unpack4(*reinterpret_cast<const uint2*>(shp + col), sh + 4 * j);
+      unpack4(*reinterpret_cast<const uint2*>(scp + col), sc + 4 * j);
+    }
   }
   float s = 0.f;
 #pragma unroll
@@ -43,22 +63,24 @@ ln_modulate_kernel(const uint16_t* __restrict__ x, long ldx, uint16_t* __restric
   }
   const float var = wave_sum(s2) / (float)H;
   const float rstd = rsqrtf(var + eps);
-  const uint16_t* shp = shift + (long)req * ld_mod;
-  const uint16_t* scp = scale + (long)req * ld_mod;
   uint16_t* op = out + (long)r * ldo;
+  float y[VPT];
 #pragma unroll
-  for (int j = 0; j < VPT / 4; ++j) {
-    const int col = (j * 64 + lane) * 4;
-    float sh[4], sc[4], y[4];
-    unpack4(*reinterpret_cast<const uint2*>(shp + col), sh);
-    unpack4(*reinterpret_cast<const uint2*>(scp + col), sc);
+  for (int t = 0; t < VPT; ++t) {
+    const float ln = mul_rn(v[t] - mean, rstd);
+    const float onep = rbf(1.0f + sc[t]);
+    y[t] = add_rn(mul_rn(ln, onep), sh[t]);
+  }
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      const float ln = mul_rn(v[4 * j + t] - mean, rstd);
-      const float onep = rbf(1.0f + sc[t]);
-      y[t] = add_rn(mul_rn(ln, onep), sh[t]);
+  for (int j = 0; j < NJ; ++j) {
+    const int col = (j * 64 + lane) * W;
+    if constexpr (W == 8) {
+      const uint2 lo = pack4(y[8 * j], y[8 * j + 1], y[8 * j + 2], y[8 * j + 3]);
+      const uint2 hi2 = pack4(y[8 * j + 4], y[8 * j + 5], y[8 * j + 6], y[8 * j + 7]);
+      *reinterpret_cast<uint4*>(op + col) = make_uint4(lo.x, lo.y, hi2.x, hi2.y);
+    } else {
+      *reinterpret_cast<uint2*>(op + col) = pack4(y[4 * j], y[4 * j + 1], y[4 * j + 2], y[4 * j + 3]);
     }
-    *reinterpret_cast<uint2*>(op + col) = pack4(y[0], y[1], y[2], y[3]);
   }
 }
 
