@@ -12,10 +12,13 @@
 // softmax(q k^T / 8) v with an online (flash) softmax.
 //
 // Work split: one workgroup = 128 query rows of one (sequence, head); wave w
-// owns 32 of them. Workgroups are numbered so that every query tile of one
-// (sequence, head) runs on the same XCD (workgroup i goes to XCD i % 8), where
-// the K/V tiles they share stay in that XCD's L2; (sequence, head) pairs are
-// dealt round-robin over the XCDs and each pair's longest query tiles come first.
+// owns 32 of them. A work list (one item per existing 128-query tile, longest
+// tiles first) is built once per pass; workgroup v takes item v / heads, head
+// v % heads, so the dispatcher hands out the longest tiles first and no
+// workgroup is dispatched for a tile that does not exist before all real ones.
+// Workgroup v runs on XCD v % 8; with heads a multiple of 8 every query tile of
+// one (sequence, head) runs on the same XCD, whose L2 then serves their shared
+// K/V tiles.
 //
 // Per 64-key tile, K and V^T arrive by global->LDS DMA into double-buffered,
 // XOR-swizzled tiles (16-B chunk c of row r at slot c ^ ((r >> 1) & 7), which
@@ -50,24 +53,49 @@ __device__ __forceinline__ int att_off(int r, int c) { return r * 64 + ((c ^ ((r
 // row index with bits 2 and 3 swapped
 __device__ __forceinline__ int key_perm(int x) { return (x & ~12) | ((x & 4) << 1) | ((x & 8) >> 1); }
 
+// One workgroup builds the work list: one item per 128-query tile of every
+// sequence, ordered by tile index, highest first (LDS atomics hand out slots).
+__global__ void __launch_bounds__(1024) attention_worklist_kernel(const AttnSeq* __restrict__ seqs, int n_seq,
+                                                                  char* __restrict__ list) {
+  __shared__ int s_cnt, s_levels;
+  AttnItem* items = reinterpret_cast<AttnItem*>(list + kAttnListHeader);
+  if (threadIdx.x == 0) { s_cnt = 0; s_levels = 0; }
+  __syncthreads();
+  for (int i = threadIdx.x; i < n_seq; i += blockDim.x)
+    atomicMax(&s_levels, (seqs[i].q_end - seqs[i].q_begin + BQ - 1) / BQ);
+  __syncthreads();
+  for (int lv = s_levels - 1; lv >= 0; --lv) {
+    for (int i = threadIdx.x; i < n_seq; i += blockDim.x) {
+      const AttnSeq sq = seqs[i];
+      if ((sq.q_end - sq.q_begin + BQ - 1) / BQ > lv) {
+        AttnItem it;
+        it.seq = sq;
+        it.tile = lv;
+#pragma unroll
+        for (int k = 0; k < 7; ++k) it.pad[k] = 0;
+        items[atomicAdd(&s_cnt, 1)] = it;
+      }
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) *reinterpret_cast<int*>(list) = s_cnt;
+}
+
 __global__ void __launch_bounds__(256, 3)
 seq_attention_kernel(const uint16_t* __restrict__ qk, long ldqk, const uint16_t* __restrict__ vt,
-                     long ld_vt, uint16_t* __restrict__ out, long ldo, const AttnSeq* __restrict__ seqs,
-                     int n_seq, int heads, int nq, float scale_log2) {
+                     long ld_vt, uint16_t* __restrict__ out, long ldo, int heads,
+                     const char* __restrict__ list, float scale_log2) {
   __shared__ __attribute__((aligned(16))) uint16_t K0[BKV * HD];
   __shared__ __attribute__((aligned(16))) uint16_t K1[BKV * HD];
   __shared__ __attribute__((aligned(16))) uint16_t V0[HD * BKV];
   __shared__ __attribute__((aligned(16))) uint16_t V1[HD * BKV];
 
-  const int xcd = blockIdx.x % NXCD;
-  const int slot = blockIdx.x / NXCD;
-  const int pair = (slot / nq) * NXCD + xcd;
-  if (pair >= n_seq * heads) return;
-  const int qt = nq - 1 - slot % nq;  // longest (last) query tiles first
-  const int h = pair % heads;
-  const AttnSeq sq = seqs[pair / heads];
-  const int q0 = sq.q_begin + qt * BQ;
-  if (q0 >= sq.q_end) return;
+  const int v = blockIdx.x;
+  if (v >= *reinterpret_cast<const int*>(list) * heads) return;
+  const AttnItem item = reinterpret_cast<const AttnItem*>(list + kAttnListHeader)[v / heads];
+  const int h = v % heads;
+  const AttnSeq sq = item.seq;
+  const int q0 = sq.q_begin + item.tile * BQ;
   const int T = sq.kv_len;           // keys of full rows
   const int cend = sq.causal_end;    // queries below this are causal
   const int H = heads * HD;
@@ -376,16 +404,20 @@ decode_combine_kernel(const float* __restrict__ part, const AttnSeq* __restrict_
 
 }  // namespace
 
+hipError_t attention_worklist(const AttnSeq* seqs, int n_seq, void* list, hipStream_t s) {
+  if (n_seq < 0 || n_seq >= (1 << 24)) return hipErrorInvalidValue;
+  dfh_launch(attention_worklist_kernel, dim3(1), dim3(1024), 0, s, seqs, n_seq, reinterpret_cast<char*>(list));
+  return hipGetLastError();
+}
+
 hipError_t seq_attention(const uint16_t* qk, long ldqk, const uint16_t* vt, long ld_vt, uint16_t* out,
-                         long ldo, const AttnSeq* seqs, int n_seq, int heads, int max_q, hipStream_t s) {
-  if (n_seq <= 0 || max_q <= 0) return hipSuccess;
+                         long ldo, int heads, const void* list, long max_items, hipStream_t s) {
+  if (max_items <= 0) return hipSuccess;
   const float scale_log2 = 0.125f * 1.4426950408889634f;  // head_dim^-0.5 * log2(e)
-  const int nq = (max_q + BQ - 1) / BQ;
-  const long pairs = (long)n_seq * heads;
-  const long grid = (pairs + NXCD - 1) / NXCD * NXCD * nq;
+  const long grid = max_items * heads;
   if (grid > 0x7fffffffL) return hipErrorInvalidValue;
-  dfh_launch(seq_attention_kernel, dim3((unsigned)grid), dim3(256), 0, s, qk, ldqk, vt, ld_vt, out, ldo, seqs,
-             n_seq, heads, nq, scale_log2);
+  dfh_launch(seq_attention_kernel, dim3((unsigned)grid), dim3(256), 0, s, qk, ldqk, vt, ld_vt, out, ldo, heads,
+             reinterpret_cast<const char*>(list), scale_log2);
   return hipGetLastError();
 }
 

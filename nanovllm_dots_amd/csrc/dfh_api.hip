@@ -97,6 +97,7 @@ struct DfhHandle {
   DevBuf temb_in, t_hid, t_out, d_hid, d_out, cond, cond_act, mod;
   DevBuf z, zp, fin, vel, tvals;
   DevBuf splitws;  // K-split: tile counters, then a 256x256 f32 partial tile per resident workgroup
+  DevBuf attq;     // attention work list: item count, then one AttnItem per 128-query tile
   bool ksplit = true;
 
   // profiling
@@ -185,6 +186,7 @@ int reserve_rows(DfhHandle* h, long M, hipStream_t s) {
   DFH_CHECK(dev_alloc(h->ff, M * F * 2));
   DFH_CHECK(dev_alloc(h->row_req, M * 4));
   DFH_CHECK(dev_alloc(h->row_pos, M * 4));
+  DFH_CHECK(dev_alloc(h->attq, kAttnListHeader + M * sizeof(AttnItem)));  // at most one item per query row
   DFH_CHECK(dev_alloc(h->vt_col, M * 4));
   DFH_CHECK(dev_alloc(h->fin, M * H * 2));
   DFH_CHECK(dev_alloc(h->vel, M * ld * 2));
@@ -307,6 +309,8 @@ int run_blocks(DfhHandle* h, const Pass& p, hipStream_t s) {
   const long ldm = h->ld_mod;
   const int* row_req = p.row_req;
 
+  // attention work list of this pass (its sequences are fixed for all blocks)
+  if (!p.decode) DFH_CHECK(attention_worklist(p.seqs, p.n_seq, h->attq.p, s));
   // input_layer
   DFH_CHECK(gemm(h, PC_OTHER, linear_args(P<uint16_t>(h->seq), H, h->in_w, h->in_b,
                                           P<uint16_t>(h->x), H, Mup, Md, H, H), EPI_BIAS, s,
@@ -332,8 +336,8 @@ int run_blocks(DfhHandle* h, const Pass& p, hipStream_t s) {
       DFH_CHECK(decode_attention(p.qk[l], p.ldqk, p.vt[l], p.ld_vt, P<uint16_t>(h->attn), H, p.seqs, p.n_seq,
                                  c.heads, p.max_kv, p.part, s));
     else
-      DFH_CHECK(seq_attention(p.qk[l], p.ldqk, p.vt[l], p.ld_vt, P<uint16_t>(h->attn), H, p.seqs, p.n_seq,
-                              c.heads, p.max_q, s));
+      DFH_CHECK(seq_attention(p.qk[l], p.ldqk, p.vt[l], p.ld_vt, P<uint16_t>(h->attn), H, c.heads, h->attq.p,
+                              (long)p.n_seq * ((p.max_q + 127) / 128), s));
     GemmArgs o = linear_args(P<uint16_t>(h->attn), H, h->o_w[l], h->o_b[l], P<uint16_t>(h->x), H,
                              Mup, Md, H, H);
     o.gate = ml + 2 * H; o.ld_gate = ldm; o.row_req = row_req;
@@ -423,7 +427,7 @@ int dfh_destroy(DfhHandle* h) {
                     &h->vt, &h->row_req, &h->row_pos, &h->vt_col, &h->cu_rows, &h->cu_vt,
                     &h->hist_len, &h->counts, &h->err, &h->patch_rows, &h->seqs, &h->rope_cos, &h->rope_sin,
                     &h->temb_in, &h->t_hid, &h->t_out, &h->d_hid, &h->d_out, &h->cond,
-                    &h->cond_act, &h->mod, &h->z, &h->zp, &h->fin, &h->vel, &h->tvals, &h->splitws};
+                    &h->cond_act, &h->mod, &h->z, &h->zp, &h->fin, &h->vel, &h->tvals, &h->splitws, &h->attq};
   for (DevBuf* b : bufs)
     if (b->p) (void)hipFree(b->p);
   for (hipEvent_t ev : h->ev_pool) (void)hipEventDestroy(ev);

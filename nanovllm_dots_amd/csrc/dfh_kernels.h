@@ -91,10 +91,24 @@ struct AttnSeq {
   int out_row0;    // output row of query position 0
 };
 
+// Work list of seq_attention: word 0 the item count, then from byte 64 one
+// AttnItem per 128-query tile of a sequence, longest tiles (the highest tile
+// index of any sequence) first. At most one item per query row, so
+// 64 + 64 * (query rows of all sequences) bytes suffice.
+struct AttnItem {
+  AttnSeq seq;
+  int tile;  // 128-query tile index within the sequence
+  int pad[7];
+};
+constexpr int kAttnListHeader = 64;  // bytes before the first item
+hipError_t attention_worklist(const AttnSeq* seqs, int n_seq, void* list, hipStream_t s);
+
 // Varlen attention with the implicit FM mask (head_dim 64), one workgroup per
-// 128 queries of one (sequence, head). max_q bounds q_end - q_begin.
+// 128 queries of one (sequence, head): workgroup v takes item v / heads of
+// `list` (attention_worklist of the same sequences), head v % heads.
+// max_items bounds the item count of the list (e.g. n_seq * ceil(max_q / 128)).
 hipError_t seq_attention(const uint16_t* qk, long ldqk, const uint16_t* vt, long ld_vt, uint16_t* out,
-                         long ldo, const AttnSeq* seqs, int n_seq, int heads, int max_q, hipStream_t s);
+                         long ldo, int heads, const void* list, long max_items, hipStream_t s);
 
 // Split-KV decode attention: every query of a sequence sees all kv_len keys
 // (q_begin..q_end are at most 32 queries). Keys are read straight from HBM in
