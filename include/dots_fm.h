@@ -11,6 +11,9 @@
  *   dfh_meanflow_solve  <- GraphedMeanflow.__call__
  *                          nanovllm_dots/models/dots/graphed_meanflow.py:36-60, and
  *                          batched_meanflow nanovllm_dots/models/dots/batched_fm.py:82-126
+ *   dfh_meanflow_solve_varlen
+ *                       <- DotsBatchEngine._pack_fm_inputs + the solve call
+ *                          nanovllm_dots/models/dots/engine.py:635-688, 713-724
  *   dfh_dit_forward     <- DiT.forward (the `vfp` callable)
  *                          nanovllm_dots/models/dots/native/dit.py:135-148
  *   dfh_set_weights     <- build_native_dit / load_component weight binding
@@ -92,6 +95,32 @@ typedef struct DfhSolveArgs {
   const float* dt_grid;        /* host [num_steps]: t_{s+1} - t_s */
 } DfhSolveArgs;
 
+/* Whole MeanFlow solve over N requests handed over as they sit in the engine
+ * (varlen): request i's c_i = hist_len[i] history rows start at hist_rows[i],
+ * row stride row_stride elements; no padded batch, no mask, no pos_ids.
+ * This replaces the padding half of DotsBatchEngine._pack_fm_inputs
+ * (engine.py:635-688: the per-request copies of fm_sequence[0, :L] into a
+ * zero [n, max_len + P, H] batch, the [n, T, T] mask and pos_ids built by
+ * _build_fm_attn_mask / _build_fm_pos_ids, native/model.py:57-87). The result
+ * equals dfh_meanflow_solve on the padded batch of the same requests, bit for bit.
+ * hist_rows: 16-B aligned bases; row_stride >= hidden, a multiple of 8.
+ * A length outside [1, max_hist] or a misaligned base is reported by
+ * dfh_input_status (bits 0 and 1), like a bad pos_ids in dfh_meanflow_solve;
+ * such a request is solved with its first history row only (or zero rows). */
+typedef struct DfhVarlenSolveArgs {
+  int n;                    /* requests */
+  int max_hist;             /* >= every c_i (sizes the workspace) */
+  int num_steps;            /* NFE (<= 16) */
+  const void* const* hist_rows;  /* device array [n] of device pointers to bf16 rows */
+  const int* hist_len;           /* device int32 [n]: c_i */
+  long row_stride;               /* elements between consecutive history rows */
+  const void* g_cond;            /* bf16 [n, H] or NULL (zeros) */
+  const void* noise;             /* bf16 [n, P, ld] */
+  void* out;                     /* bf16 [n, P, ld] */
+  const float* t_grid;           /* host [num_steps]: t_s */
+  const float* dt_grid;          /* host [num_steps]: t_{s+1} - t_s */
+} DfhVarlenSolveArgs;
+
 /* One DiT forward (the vfp callable) on the padded layout. */
 typedef struct DfhForwardArgs {
   int n;
@@ -115,6 +144,7 @@ int dfh_set_weights(DfhHandle* h, const DfhWeights* w, void* stream);
  * solver steps (synchronizes the stream only when it grows). */
 int dfh_reserve(DfhHandle* h, int n, int total_len, int num_steps, void* stream);
 int dfh_meanflow_solve(DfhHandle* h, const DfhSolveArgs* a, void* stream);
+int dfh_meanflow_solve_varlen(DfhHandle* h, const DfhVarlenSolveArgs* a, void* stream);
 int dfh_dit_forward(DfhHandle* h, const DfhForwardArgs* a, void* stream);
 /* Reads and clears the device-side input check of the last solve/forward
  * (bit 0: a pos_ids row does not describe a valid FM layout). Synchronizes. */

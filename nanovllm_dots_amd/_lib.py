@@ -45,6 +45,15 @@ class DfhSolveArgs(C.Structure):
     ]
 
 
+class DfhVarlenSolveArgs(C.Structure):
+    _fields_ = [
+        ("n", C.c_int), ("max_hist", C.c_int), ("num_steps", C.c_int),
+        ("hist_rows", vp), ("hist_len", vp), ("row_stride", C.c_long),
+        ("g_cond", vp), ("noise", vp), ("out", vp),
+        ("t_grid", C.POINTER(C.c_float)), ("dt_grid", C.POINTER(C.c_float)),
+    ]
+
+
 class DfhForwardArgs(C.Structure):
     _fields_ = [
         ("n", C.c_int), ("total_len", C.c_int), ("x", vp), ("timesteps", vp), ("duration", vp),
@@ -60,6 +69,7 @@ SIGNATURES = {
     "dfh_set_weights": (C.c_int, [vp, C.POINTER(DfhWeights), vp]),
     "dfh_reserve": (C.c_int, [vp, C.c_int, C.c_int, C.c_int, vp]),
     "dfh_meanflow_solve": (C.c_int, [vp, C.POINTER(DfhSolveArgs), vp]),
+    "dfh_meanflow_solve_varlen": (C.c_int, [vp, C.POINTER(DfhVarlenSolveArgs), vp]),
     "dfh_dit_forward": (C.c_int, [vp, C.POINTER(DfhForwardArgs), vp]),
     "dfh_input_status": (C.c_int, [vp, C.POINTER(C.c_int), vp]),
     "dfh_profile_enable": (C.c_int, [vp, C.c_int]),

@@ -377,18 +377,53 @@ int dit_blocks(DfhHandle* h, int n, int T, long mod_row0, hipStream_t s) {
   return run_blocks(h, p, s);
 }
 
-int layout(DfhHandle* h, int n, int T, const void* pos_ids, const void* inp, hipStream_t s) {
+// Packed layout of n requests, T = max history + P. Padded inputs: pos_ids and
+// inp [n, T, H]. Varlen inputs: lens [n] and the history bases src_rows [n].
+int layout(DfhHandle* h, int n, int T, const void* pos_ids, const void* inp, hipStream_t s,
+           const int* lens = nullptr, const uint16_t* const* src_rows = nullptr, long src_stride = 0) {
   const DfhConfig& c = h->cfg;
-  DFH_CHECK(fm_layout(reinterpret_cast<const float*>(pos_ids), n, T, c.patch, P<int>(h->cu_rows),
+  DFH_CHECK(fm_layout(reinterpret_cast<const float*>(pos_ids), lens, n, T, c.patch, P<int>(h->cu_rows),
                       P<int>(h->cu_vt), P<int>(h->hist_len), P<int>(h->counts), P<int>(h->err),
                       P<AttnSeq>(h->seqs), s));
-  DFH_CHECK(fm_gather(reinterpret_cast<const uint16_t*>(inp), n, T, c.patch, c.hidden,
+  DFH_CHECK(fm_gather(reinterpret_cast<const uint16_t*>(inp), src_rows, src_stride, n, T, c.patch, c.hidden,
                       P<int>(h->cu_rows), P<int>(h->cu_vt), P<int>(h->hist_len), P<uint16_t>(h->seq),
                       P<int>(h->row_req), P<int>(h->row_pos), P<int>(h->vt_col),
-                      P<int>(h->patch_rows), s));
+                      P<int>(h->patch_rows), P<int>(h->err), s));
   if (c.rotary)
     DFH_CHECK(rope_table(P<float>(h->consts), c.head_dim / 2, T, P<float>(h->rope_cos),
                          P<float>(h->rope_sin), s));
+  return 0;
+}
+
+// The NFE steps of one MeanFlow solve on the packed layout built by layout().
+int solve_steps(DfhHandle* h, int n, int T, int S, const void* g_cond, const void* noise, void* out,
+                const float* t_grid, const float* dt_grid, hipStream_t s) {
+  const DfhConfig& c = h->cfg;
+  const int H = c.hidden, Pp = c.patch, ld = c.latent_dim;
+  // timestep rows t_0..t_{S-1} and dt_0..dt_{S-1} travel as kernel arguments
+  TimeVals tv{}, dtv{};
+  for (int k = 0; k < S; ++k) { tv.v[k] = t_grid[k]; dtv.v[k] = dt_grid[k]; }
+  if (build_modulation(h, S, n, false, nullptr, nullptr, tv, dtv, true,
+                       reinterpret_cast<const uint16_t*>(g_cond), s))
+    return 1;
+  DFH_CHECK(hipMemcpyAsync(h->z.p, noise, (size_t)n * Pp * ld * 2, hipMemcpyDeviceToDevice, s));
+  const int NP = n * Pp;
+  for (int st = 0; st < S; ++st) {
+    // zp = coordinate_proj(z) -> latent rows of the packed sequence
+    DFH_CHECK(gemm(h, PC_OTHER, linear_args(P<uint16_t>(h->z), ld, h->coord_w, h->coord_b,
+                                            P<uint16_t>(h->zp), H, NP, nullptr, H, ld), EPI_BIAS, s));
+    DFH_CHECK(scatter_rows(P<uint16_t>(h->zp), P<int>(h->patch_rows), NP, H, P<uint16_t>(h->seq), s));
+    if (dit_blocks(h, n, T, (long)st * n, s)) return 1;
+    // FinalLayer on the latent rows only
+    const uint16_t* mf = P<uint16_t>(h->mod) + (long)st * n * h->ld_mod + (long)c.n_blocks * 6 * H;
+    prof_arm(h, PC_LN);
+    DFH_CHECK(ln_modulate(P<uint16_t>(h->x), H, P<uint16_t>(h->fin), H, mf, mf + H, h->ld_mod,
+                          P<int>(h->row_req), P<int>(h->patch_rows), NP, nullptr, H, c.ln_eps, s));
+    DFH_CHECK(gemm(h, PC_OTHER, linear_args(P<uint16_t>(h->fin), H, h->fin_w, h->fin_b,
+                                            P<uint16_t>(h->vel), ld, NP, nullptr, ld, H), EPI_BIAS, s));
+    DFH_CHECK(z_update(P<uint16_t>(h->z), P<uint16_t>(h->vel), dt_grid[st], (long)NP * ld, s));
+  }
+  DFH_CHECK(hipMemcpyAsync(out, h->z.p, (size_t)NP * ld * 2, hipMemcpyDeviceToDevice, s));
   return 0;
 }
 
@@ -567,34 +602,32 @@ int dfh_meanflow_solve(DfhHandle* h, const DfhSolveArgs* a, void* stream) {
   if ((long)n * T * (c.ffn > 2 * c.hidden ? c.ffn : 2 * c.hidden) >= (1L << 31))
     return fail("dfh_meanflow_solve: n*T too large for 32-bit offsets");
   if (reserve(h, n, T, S, s)) return 1;
-  const int H = c.hidden, Pp = c.patch, ld = c.latent_dim;
-
   if (layout(h, n, T, a->pos_ids, a->input_sequence, s)) return 1;
-  // timestep rows t_0..t_{S-1} and dt_0..dt_{S-1} travel as kernel arguments
-  TimeVals tv{}, dtv{};
-  for (int k = 0; k < S; ++k) { tv.v[k] = a->t_grid[k]; dtv.v[k] = a->dt_grid[k]; }
-  if (build_modulation(h, S, n, false, nullptr, nullptr, tv, dtv, true,
-                       reinterpret_cast<const uint16_t*>(a->g_cond), s))
+  return solve_steps(h, n, T, S, a->g_cond, a->noise, a->out, a->t_grid, a->dt_grid, s);
+}
+
+int dfh_meanflow_solve_varlen(DfhHandle* h, const DfhVarlenSolveArgs* a, void* stream) {
+  if (!h || !a) return fail("null argument");
+  if (!h->weights_set) return fail("dfh_meanflow_solve_varlen: weights not set");
+  const DfhConfig& c = h->cfg;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const int n = a->n, S = a->num_steps;
+  if (n <= 0 || n > 1024 || a->max_hist <= 0 || S <= 0 || S > 16)
+    return fail("dfh_meanflow_solve_varlen: bad shape n=%d max_hist=%d steps=%d", n, a->max_hist, S);
+  if (!a->hist_rows || !a->hist_len || !a->noise || !a->out || !a->t_grid || !a->dt_grid)
+    return fail("dfh_meanflow_solve_varlen: a required pointer is NULL");
+  if (a->row_stride < c.hidden || a->row_stride % 8 != 0)
+    return fail("dfh_meanflow_solve_varlen: row_stride %ld must be >= hidden and a multiple of 8",
+                a->row_stride);
+  if (!c.meanflow) return fail("dfh_meanflow_solve_varlen: DiT has no duration embedder (not MeanFlow)");
+  const int T = a->max_hist + c.patch;
+  if ((long)n * T * (c.ffn > 2 * c.hidden ? c.ffn : 2 * c.hidden) >= (1L << 31))
+    return fail("dfh_meanflow_solve_varlen: n*T too large for 32-bit offsets");
+  if (reserve(h, n, T, S, s)) return 1;
+  if (layout(h, n, T, nullptr, nullptr, s, a->hist_len,
+             reinterpret_cast<const uint16_t* const*>(a->hist_rows), a->row_stride))
     return 1;
-  DFH_CHECK(hipMemcpyAsync(h->z.p, a->noise, (size_t)n * Pp * ld * 2, hipMemcpyDeviceToDevice, s));
-  const int NP = n * Pp;
-  for (int st = 0; st < S; ++st) {
-    // zp = coordinate_proj(z) -> latent rows of the packed sequence
-    DFH_CHECK(gemm(h, PC_OTHER, linear_args(P<uint16_t>(h->z), ld, h->coord_w, h->coord_b,
-                                            P<uint16_t>(h->zp), H, NP, nullptr, H, ld), EPI_BIAS, s));
-    DFH_CHECK(scatter_rows(P<uint16_t>(h->zp), P<int>(h->patch_rows), NP, H, P<uint16_t>(h->seq), s));
-    if (dit_blocks(h, n, T, (long)st * n, s)) return 1;
-    // FinalLayer on the latent rows only
-    const uint16_t* mf = P<uint16_t>(h->mod) + (long)st * n * h->ld_mod + (long)c.n_blocks * 6 * H;
-    prof_arm(h, PC_LN);
-    DFH_CHECK(ln_modulate(P<uint16_t>(h->x), H, P<uint16_t>(h->fin), H, mf, mf + H, h->ld_mod,
-                          P<int>(h->row_req), P<int>(h->patch_rows), NP, nullptr, H, c.ln_eps, s));
-    DFH_CHECK(gemm(h, PC_OTHER, linear_args(P<uint16_t>(h->fin), H, h->fin_w, h->fin_b,
-                                            P<uint16_t>(h->vel), ld, NP, nullptr, ld, H), EPI_BIAS, s));
-    DFH_CHECK(z_update(P<uint16_t>(h->z), P<uint16_t>(h->vel), a->dt_grid[st], (long)NP * ld, s));
-  }
-  DFH_CHECK(hipMemcpyAsync(a->out, h->z.p, (size_t)NP * ld * 2, hipMemcpyDeviceToDevice, s));
-  return 0;
+  return solve_steps(h, n, T, S, a->g_cond, a->noise, a->out, a->t_grid, a->dt_grid, s);
 }
 
 int dfh_dit_forward(DfhHandle* h, const DfhForwardArgs* a, void* stream) {

@@ -12,7 +12,8 @@ struct TimeVals {
   float v[kMaxTimeVals];
 };
 
-hipError_t fm_layout(const float* pos_ids, int n, int T, int P, int* cu_rows, int* cu_vt,
+// Request layout from pos_ids (padded inputs) or from lens (varlen inputs)
+hipError_t fm_layout(const float* pos_ids, const int* lens, int n, int T, int P, int* cu_rows, int* cu_vt,
                      int* hist_len, int* counts, int* err, AttnSeq* seqs, hipStream_t s);
 hipError_t prefix_tables(const uint16_t* rows_in, long stride_in, int m_max, int H, const int* counts,
                          const int* lens, const int* offs, int n, int S, int cap, uint16_t* seq, int* row_req,
@@ -21,9 +22,11 @@ hipError_t active_tables(const int* lens, int n, int S, int P, int cap, int* row
                          int* c_rows, int* vt_col, AttnSeq* seqs, int* patch_rows, int* lh_rows,
                          hipStream_t s);
 hipError_t cache_advance(int* lens, const int* counts, int n, hipStream_t s);
-hipError_t fm_gather(const uint16_t* inp, int n, int T, int P, int H, const int* cu_rows,
-                     const int* cu_vt, const int* hist_len, uint16_t* seq, int* row_req,
-                     int* row_pos, int* vt_col, int* patch_rows, hipStream_t s);
+// Rows from the padded input inp [n, T, H], or (inp NULL) from per-request
+// history bases src_rows[i] (device array of device pointers), row stride src_stride
+hipError_t fm_gather(const uint16_t* inp, const uint16_t* const* src_rows, long src_stride, int n, int T,
+                     int P, int H, const int* cu_rows, const int* cu_vt, const int* hist_len, uint16_t* seq,
+                     int* row_req, int* row_pos, int* vt_col, int* patch_rows, int* err, hipStream_t s);
 hipError_t rope_table(const float* inv_freq, int half, int max_pos, float* cosv, float* sinv,
                       hipStream_t s);
 hipError_t timestep_embed(const float* tv, const TimeVals& tvh, int rows, const float* freqs, int half,

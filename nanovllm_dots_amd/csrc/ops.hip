@@ -85,22 +85,31 @@ ln_modulate_kernel(const uint16_t* __restrict__ x, long ldx, uint16_t* __restric
 }
 
 // ---------------------------------------------------------------------------
-// Request layout from the padded inputs: c_i = pos_ids[i, T-P] (the first latent
-// row's position equals the history length, native/model.py:77-87).
+// Request layout. Padded inputs: c_i = pos_ids[i, T-P] (the first latent row's
+// position equals the history length, native/model.py:77-87). Varlen inputs:
+// c_i = lens[i]. A length outside [1, T-P] sets err bit 0 and is clamped into
+// it (varlen: to 1, so no more than the first row of that request is read).
 // One workgroup of up to 1024 threads, one thread per request.
 __global__ void __launch_bounds__(1024)
-fm_layout_kernel(const float* __restrict__ pos_ids, int n, int T, int P, int* __restrict__ cu_rows,
-                 int* __restrict__ cu_vt, int* __restrict__ hist_len, int* __restrict__ counts,
-                 int* __restrict__ err, AttnSeq* __restrict__ seqs) {
+fm_layout_kernel(const float* __restrict__ pos_ids, const int* __restrict__ lens, int n, int T, int P,
+                 int* __restrict__ cu_rows, int* __restrict__ cu_vt, int* __restrict__ hist_len,
+                 int* __restrict__ counts, int* __restrict__ err, AttnSeq* __restrict__ seqs) {
   __shared__ int s_rows[1024], s_vt[1024];
   const int i = threadIdx.x;
   int c = 0;
   if (i < n) {
-    const float pv = pos_ids[(long)i * T + (T - P)];
-    c = (int)pv;
-    if (!(pv >= 1.0f) || c > T - P || (float)c != pv) {
+    bool bad;
+    if (lens) {
+      c = lens[i];
+      bad = c < 1 || c > T - P;
+    } else {
+      const float pv = pos_ids[(long)i * T + (T - P)];
+      c = (int)pv;
+      bad = !(pv >= 1.0f) || c > T - P || (float)c != pv;
+    }
+    if (bad) {
       atomicOr(err, 1);
-      c = c < 1 ? 1 : (c > T - P ? T - P : c);
+      c = lens ? 1 : (c < 1 ? 1 : (c > T - P ? T - P : c));
     }
     hist_len[i] = c;
   }
@@ -132,12 +141,16 @@ fm_layout_kernel(const float* __restrict__ pos_ids, int n, int T, int P, int* __
   }
 }
 
-// Padded [N, T, H] -> packed rows; builds row tables. One wave per padded row.
+// Padded [N, T, H] (or per-request history rows src_rows[i] + r * src_stride,
+// latent slots zero) -> packed rows; builds row tables. One wave per padded row.
+// A history base that is not 16-B aligned sets err bit 1; its rows are zeroed.
 __global__ void __launch_bounds__(256)
-fm_gather_kernel(const uint16_t* __restrict__ inp, int n, int T, int P, int H,
+fm_gather_kernel(const uint16_t* __restrict__ inp, const uint16_t* const* __restrict__ src_rows,
+                 long src_stride, int n, int T, int P, int H,
                  const int* __restrict__ cu_rows, const int* __restrict__ cu_vt,
                  const int* __restrict__ hist_len, uint16_t* __restrict__ seq, int* __restrict__ row_req,
-                 int* __restrict__ row_pos, int* __restrict__ vt_col, int* __restrict__ patch_rows) {
+                 int* __restrict__ row_pos, int* __restrict__ vt_col, int* __restrict__ patch_rows,
+                 int* __restrict__ err) {
   const int lane = threadIdx.x & 63;
   const long pr = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (pr >= (long)n * T) return;
@@ -155,9 +168,14 @@ fm_gather_kernel(const uint16_t* __restrict__ inp, int n, int T, int P, int H,
     if (local >= c) patch_rows[i * P + (local - c)] = dst;
   }
   const uint16_t* sp = inp + pr * H;
+  if (src_rows) {
+    const uint16_t* base = src_rows[i];
+    sp = local < c && ((uintptr_t)base & 15) == 0 ? base + (long)local * src_stride : nullptr;
+    if (local < c && !sp && lane == 0) atomicOr(err, 2);
+  }
   uint16_t* dp = seq + (long)dst * H;
   for (int col = lane * 8; col < H; col += 64 * 8)
-    *reinterpret_cast<uint4*>(dp + col) = *reinterpret_cast<const uint4*>(sp + col);
+    *reinterpret_cast<uint4*>(dp + col) = sp ? *reinterpret_cast<const uint4*>(sp + col) : make_uint4(0u, 0u, 0u, 0u);
 }
 
 // packed [M, D] rows -> padded [n, T, D]; rows of the padding gap are zero-filled.
@@ -381,21 +399,23 @@ hipError_t ln_modulate(const uint16_t* x, long ldx, uint16_t* out, long ldo, con
   return hipGetLastError();
 }
 
-hipError_t fm_layout(const float* pos_ids, int n, int T, int P, int* cu_rows, int* cu_vt,
+hipError_t fm_layout(const float* pos_ids, const int* lens, int n, int T, int P, int* cu_rows, int* cu_vt,
                      int* hist_len, int* counts, int* err, AttnSeq* seqs, hipStream_t s) {
-  if (n <= 0 || n > 1024) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(fm_layout_kernel, dim3(1), dim3(1024), 0, s, pos_ids, n, T, P, cu_rows, cu_vt,
+  if (n <= 0 || n > 1024 || (!pos_ids && !lens)) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(fm_layout_kernel, dim3(1), dim3(1024), 0, s, pos_ids, lens, n, T, P, cu_rows, cu_vt,
                      hist_len, counts, err, seqs);
   return hipGetLastError();
 }
 
-hipError_t fm_gather(const uint16_t* inp, int n, int T, int P, int H, const int* cu_rows,
-                     const int* cu_vt, const int* hist_len, uint16_t* seq, int* row_req,
-                     int* row_pos, int* vt_col, int* patch_rows, hipStream_t s) {
+hipError_t fm_gather(const uint16_t* inp, const uint16_t* const* src_rows, long src_stride, int n, int T,
+                     int P, int H, const int* cu_rows, const int* cu_vt, const int* hist_len, uint16_t* seq,
+                     int* row_req, int* row_pos, int* vt_col, int* patch_rows, int* err, hipStream_t s) {
   const long rows = (long)n * T;
-  if (H % 8 != 0) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(fm_gather_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, s, inp, n, T,
-                     P, H, cu_rows, cu_vt, hist_len, seq, row_req, row_pos, vt_col, patch_rows);
+  if (H % 8 != 0 || (!inp && !src_rows) || (src_rows && (src_stride < H || src_stride % 8 != 0)))
+    return hipErrorInvalidValue;
+  hipLaunchKernelGGL(fm_gather_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, s, inp, src_rows,
+                     src_stride, n, T, P, H, cu_rows, cu_vt, hist_len, seq, row_req, row_pos, vt_col,
+                     patch_rows, err);
   return hipGetLastError();
 }
 

@@ -199,6 +199,55 @@ class HipFMHead:
             self._raise_input_status(st)
         return out
 
+    def solve_varlen(self, sequences, lengths, g_cond, noise, num_steps: int, *, strict=False):
+        """One solve over requests as the engine holds them: request i's history is
+        the first ``lengths[i]`` rows of ``sequences[i]`` (``[L, H]`` or ``[1, L, H]``
+        bf16 on the GPU, e.g. ``fm_sequence``). No padded batch, mask or pos_ids is
+        built (engine.py:635-688); the result equals :meth:`solve` on the padded
+        batch of the same requests."""
+        s = self.spec
+        n = len(sequences)
+        if n == 0 or len(lengths) != n:
+            raise RuntimeError(f"need one length per sequence, got {n} sequences and {len(lengths)} lengths")
+        rows = [q[0] if q.dim() == 3 else q for q in sequences]
+        stride = None
+        for q, L in zip(rows, lengths):
+            if q.dim() != 2 or q.shape[1] != s.hidden or q.dtype != torch.bfloat16 or not q.is_cuda:
+                raise RuntimeError(f"each sequence must be a bf16 [L, {s.hidden}] GPU tensor, got "
+                                   f"{tuple(q.shape)} {q.dtype} on {q.device}")
+            if not 1 <= int(L) <= q.shape[0]:
+                raise RuntimeError(f"history length {int(L)} outside [1, {q.shape[0]}]")
+            if stride is None:
+                stride = q.stride(0)
+            if q.stride(1) != 1 or q.stride(0) != stride or q.data_ptr() % 16 or stride % 8:
+                # one row stride for every request, 16-B aligned rows
+                stride = None
+                break
+        if stride is None:
+            rows = [q[:int(L)].contiguous() for q, L in zip(rows, lengths)]
+            stride = s.hidden
+        if noise.shape != (n, s.patch, s.latent_dim):
+            raise RuntimeError(f"noise shape {tuple(noise.shape)} != {(n, s.patch, s.latent_dim)}")
+        dev = rows[0].device
+        ptrs = torch.tensor([q.data_ptr() for q in rows], dtype=torch.int64).to(dev)
+        lens = torch.tensor([int(L) for L in lengths], dtype=torch.int32).to(dev)
+        g = g_cond.reshape(n, s.hidden).to(torch.bfloat16).contiguous() if g_cond is not None else None
+        nz = noise.to(torch.bfloat16).contiguous()
+        out = torch.empty((n, s.patch, s.latent_dim), device=dev, dtype=torch.bfloat16)
+        ts, dts = meanflow_grid(num_steps)
+        tg = (C.c_float * num_steps)(*ts)
+        dg = (C.c_float * num_steps)(*dts)
+        args = _lib.DfhVarlenSolveArgs(n=n, max_hist=max(int(L) for L in lengths), num_steps=num_steps,
+                                       hist_rows=_lib.ptr(ptrs), hist_len=_lib.ptr(lens), row_stride=stride,
+                                       g_cond=_lib.ptr(g), noise=_lib.ptr(nz), out=_lib.ptr(out),
+                                       t_grid=tg, dt_grid=dg)
+        st = _lib.stream_ptr()
+        _lib.check(self.lib.dfh_meanflow_solve_varlen(self.handle, C.byref(args), st),
+                   "dfh_meanflow_solve_varlen")
+        if strict:
+            self._raise_input_status(st)
+        return out
+
     def forward(self, x, timesteps, duration, pos_ids, g_cond, *, strict=False):
         s = self.spec
         n, T, H = x.shape
@@ -269,9 +318,11 @@ class HipFMHead:
     def _raise_input_status(self, st):
         flags = C.c_int(0)
         _lib.check(self.lib.dfh_input_status(self.handle, C.byref(flags), st), "dfh_input_status")
-        if flags.value:
-            raise RuntimeError("pos_ids does not describe a valid FM layout "
-                               "(history length c = pos_ids[i, T-P] must be an integer in [1, T-P])")
+        if flags.value & 1:
+            raise RuntimeError("the inputs do not describe a valid FM layout (history length "
+                               "c = pos_ids[i, T-P], or hist_len[i], must be an integer in [1, T-P])")
+        if flags.value & 2:
+            raise RuntimeError("a history row base is not 16-byte aligned")
 
 
 def _weights_from_modules(dit, core) -> dict[str, torch.Tensor]:
@@ -310,6 +361,20 @@ class HipMeanflow:
             noise = torch.randn((n, self.patch, self.latent_dim), device=input_sequence.device,
                                 dtype=input_sequence.dtype)
         return self.head.solve(input_sequence, pos_ids, g_cond, noise, self.nfe, strict=self.strict)
+
+
+    @torch.no_grad()
+    def solve_varlen(self, *, sequences, lengths, g_cond=None, num_steps=None, noise=None):
+        """The whole solve straight from per-request histories (``fm_sequence``,
+        ``fm_seq_len``), in place of ``_pack_fm_inputs`` + ``__call__``
+        (engine.py:635-688, :713-724). Same noise and NFE rules as ``__call__``."""
+        if num_steps is not None and num_steps != self.nfe:
+            raise RuntimeError(f"HipMeanflow built for nfe={self.nfe}, got {num_steps}.")
+        n = len(sequences)
+        if noise is None:
+            noise = torch.randn((n, self.patch, self.latent_dim), device=sequences[0].device,
+                                dtype=torch.bfloat16)
+        return self.head.solve_varlen(sequences, lengths, g_cond, noise, self.nfe, strict=self.strict)
 
 
 class HipDiT:
