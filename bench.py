@@ -175,6 +175,76 @@ def kvcache_bench(head, cfg, reps: int = 10):
     return res
 
 
+def paged_bench(reps: int = 20):
+    """Paged KV-cache attention of the LLM backbone (Qwen2.5-1.5B: 12 query heads,
+    2 KV heads, head_dim 128, 256-token pages), 64 sequences x 4096 cached keys in
+    shuffled pages: decode (1 new token each) and a 4-token append. Called through
+    the C ABI with every argument built once, so the time is the kernels'.
+    HBM-bound: the compulsory bytes are every K and V row once, plus q and out."""
+    import ctypes as C
+    import torch
+    from nanovllm_dots_amd import _lib
+    lib = _lib.lib()
+    B, H, Hkv, hd, bs, L = 64, 12, 2, 128, 256, 4096
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(0)
+    pages = B * L // bs
+    kc = torch.randn(pages, bs, Hkv, hd, device=dev, generator=g).bfloat16()
+    vc = torch.randn(pages, bs, Hkv, hd, device=dev, generator=g).bfloat16()
+    bt = torch.randperm(pages, device=dev, generator=g).to(torch.int32).view(B, L // bs).contiguous()
+    lens = torch.full((B,), L, dtype=torch.int32, device=dev)
+    res = {"config": "64 seqs x 4096 keys in shuffled 256-token pages, 12/2 heads, head_dim 128"}
+    for name, lq in (("decode", 1), ("append4", 4)):
+        q = torch.randn(B * lq, H, hd, device=dev, generator=g).bfloat16()
+        out = torch.empty_like(q)
+        cu_q = torch.arange(0, (B + 1) * lq, lq, dtype=torch.int32, device=dev)
+        a = _lib.DfhPagedAttnArgs(batch=B, num_heads=H, num_kv_heads=Hkv, head_dim=hd, max_seqlen_q=lq,
+                                  max_seqlen_k=L, q=_lib.ptr(q), q_stride=H * hd, cu_seqlens_q=_lib.ptr(cu_q),
+                                  k=_lib.ptr(kc), v=_lib.ptr(vc), kv_stride=Hkv * hd, cu_seqlens_k=None,
+                                  seqlens_k=_lib.ptr(lens), block_table=_lib.ptr(bt), block_table_stride=L // bs,
+                                  block_size=bs, out=_lib.ptr(out), out_stride=H * hd, softmax_scale=hd ** -0.5,
+                                  causal=1, workspace=None, workspace_bytes=0)
+        ws = torch.empty(lib.dfh_paged_attention_workspace(C.byref(a)) // 4, device=dev)
+        a.workspace, a.workspace_bytes = _lib.ptr(ws), ws.numel() * 4
+        st = _lib.stream_ptr()
+        for _ in range(3):
+            _lib.check(lib.dfh_paged_attention(C.byref(a), st), "dfh_paged_attention")
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            lib.dfh_paged_attention(C.byref(a), st)
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) / reps * 1e3
+        nbytes = 2 * B * L * Hkv * hd * 2 + 2 * 2 * B * lq * H * hd
+        res[name] = {"us_per_call": round(us, 2), "GB_s": round(nbytes / us / 1e3, 1),
+                     "frac_hbm": round(nbytes / us / 1e3 / PEAK_HBM_GBS, 4), "algorithmic_bytes": nbytes}
+    log(f"paged: {res}")
+    return res
+
+
+def varlen_bench(mf, hist, noise_d, g_d, ref_out, reps: int = 5):
+    """The same C3 solve from per-request history tensors (dfh_meanflow_solve_varlen):
+    no padded [N,T,H] batch, [N,T,T] mask or pos_ids exists."""
+    import torch
+    dev = noise_d.device
+    seqs = [h.to(dev, torch.bfloat16) for h in hist]
+    lens = [h.shape[0] for h in hist]
+    out = mf.solve_varlen(sequences=seqs, lengths=lens, g_cond=g_d, noise=noise_d)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        out = mf.solve_varlen(sequences=seqs, lengths=lens, g_cond=g_d, noise=noise_d)
+    e1.record()
+    torch.cuda.synchronize()
+    res = {"ms_per_solve": round(e0.elapsed_time(e1) / reps, 4),
+           "bit_identical_to_padded": bool(torch.equal(out, ref_out))}
+    log(f"varlen: {res}")
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -186,6 +256,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-w8a8", action="store_true")
     ap.add_argument("--no-kvcache", action="store_true")
+    ap.add_argument("--no-paged", action="store_true")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="run a device copy of this size first (HBM counter calibration under rocprofv3)")
     args = ap.parse_args()
@@ -273,6 +344,8 @@ def main():
     gemm_ms = sum(role_ms.values()) / args.steps
     log("per-class ms/solve: " + ", ".join(f"{k}={v['ms_per_solve']:.3f}" for k, v in breakdown.items()))
 
+    vl = varlen_bench(mf, hist, noise_d, g_d, out)
+    pg = None if args.no_paged else paged_bench()
     w8 = None if args.no_w8a8 else w8a8_bench()
     kvc = None if args.no_kvcache else kvcache_bench(head, cfg)
 
@@ -302,6 +375,8 @@ def main():
         "kernel_breakdown": breakdown,
         "w8a8_m16384": w8,
         "kvcache_4x10111": kvc,
+        "varlen_solve": vl,
+        "llm_paged_attention": pg,
         "cpu_baseline": ({k: (round(v, 5) if isinstance(v, float) else v) for k, v in cpu.items()
                           if k in ("value", "unit", "cores", "kind", "sample")} if cpu else None),
         "cpu_xRT": round(cpu["xRT"], 4) if cpu else None,

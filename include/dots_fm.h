@@ -22,6 +22,9 @@
  *                          nanovllm_dots/models/dots/native/layers.py:82-84, 152-161
  *   dfh_quant_act_i8, dfh_quant_weight_i8, dfh_gemm_w8a8
  *                       <- Int8DynamicLinear nanovllm_dots/models/dots/int8_dit.py:34-65
+ *   dfh_store_kvcache   <- store_kvcache nanovllm_dots/layers/attention.py:10-47
+ *   dfh_paged_attention <- flash_attn_varlen_func / flash_attn_with_kvcache as called
+ *                          by Attention.forward nanovllm_dots/layers/attention.py:66-95
  *   dfh_kvcache_*       <- FMCache / extend_cache / active_forward
  *                          nanovllm_dots/models/dots/cached_fm.py:82-197 (CFG flow matching
  *                          there; restated for the MeanFlow DiT)
@@ -211,6 +214,52 @@ int dfh_kvcache_extend(DfhKVCache* c, const void* rows, int m_max, const int* co
                        const float* t_grid, const float* dt_grid, void* stream);
 int dfh_kvcache_solve(DfhKVCache* c, const void* last_hidden, const void* g_cond, const void* noise, void* out,
                       const float* t_grid, const float* dt_grid, void* stream);
+
+/* Paged KV cache of the LLM backbone (Qwen2.5-1.5B: 12 query heads, 2 KV heads,
+ * head_dim 128, 256-token pages).
+ *
+ * dfh_store_kvcache <- store_kvcache, nanovllm_dots/layers/attention.py:10-47:
+ * key / value rows i (D = kv_heads * head_dim bf16, row strides in elements)
+ * go to row slot_mapping[i] of k_cache / v_cache ([num_slots, D]); slot -1
+ * skips the token. D and the strides multiples of 8, bases 16-B aligned. */
+int dfh_store_kvcache(const void* key, long key_stride, const void* value, long value_stride, void* k_cache,
+                      void* v_cache, const int* slot_mapping, int n_tokens, int D, void* stream);
+
+/* dfh_paged_attention <- flash_attn_varlen_func (with or without block_table)
+ * and flash_attn_with_kvcache (k = v = None) as layers/attention.py:66-95 call
+ * them (flash-attn 2.8.3). Sequence i: query tokens cu_seqlens_q[i] ..
+ * cu_seqlens_q[i+1] of q, Lk_i keys (cu_seqlens_k diff, or seqlens_k[i] =
+ * cache_seqlens). Key t: page block_table[i][t / block_size], offset
+ * t % block_size, of k_cache / v_cache [num_blocks, block_size, kv_heads,
+ * head_dim]; with block_table NULL, row cu_seqlens_k[i] + t of k / v
+ * [total_k, kv_heads, head_dim]. causal: bottom-right aligned (token j of Lq
+ * sees keys [0, Lk - Lq + j]); a row that sees no key is written as 0. Query
+ * head h reads KV head h / (num_heads / num_kv_heads). out [total_q, num_heads,
+ * head_dim] bf16. head_dim 64 or 128; block_size a multiple of 256; q, k, v
+ * 16-B aligned, strides (elements between tokens) multiples of 8. The
+ * workspace holds dfh_paged_attention_workspace(a) bytes. */
+typedef struct DfhPagedAttnArgs {
+  int batch, num_heads, num_kv_heads, head_dim;
+  int max_seqlen_q, max_seqlen_k;   /* host upper bounds */
+  const void* q;
+  long q_stride;
+  const int* cu_seqlens_q;          /* int32 [batch + 1] device */
+  const void* k;
+  const void* v;
+  long kv_stride;
+  const int* cu_seqlens_k;          /* int32 [batch + 1] device, or NULL (then seqlens_k) */
+  const int* seqlens_k;             /* int32 [batch] device, or NULL */
+  const int* block_table;           /* int32 [batch, block_table_stride] device, or NULL */
+  int block_table_stride, block_size;
+  void* out;
+  long out_stride;
+  float softmax_scale;
+  int causal;
+  void* workspace;
+  long workspace_bytes;
+} DfhPagedAttnArgs;
+long dfh_paged_attention_workspace(const DfhPagedAttnArgs* a);
+int dfh_paged_attention(const DfhPagedAttnArgs* a, void* stream);
 
 #ifdef __cplusplus
 }

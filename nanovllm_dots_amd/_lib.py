@@ -54,6 +54,19 @@ class DfhVarlenSolveArgs(C.Structure):
     ]
 
 
+class DfhPagedAttnArgs(C.Structure):
+    _fields_ = [
+        ("batch", C.c_int), ("num_heads", C.c_int), ("num_kv_heads", C.c_int), ("head_dim", C.c_int),
+        ("max_seqlen_q", C.c_int), ("max_seqlen_k", C.c_int),
+        ("q", vp), ("q_stride", C.c_long), ("cu_seqlens_q", vp),
+        ("k", vp), ("v", vp), ("kv_stride", C.c_long),
+        ("cu_seqlens_k", vp), ("seqlens_k", vp), ("block_table", vp),
+        ("block_table_stride", C.c_int), ("block_size", C.c_int),
+        ("out", vp), ("out_stride", C.c_long), ("softmax_scale", C.c_float), ("causal", C.c_int),
+        ("workspace", vp), ("workspace_bytes", C.c_long),
+    ]
+
+
 class DfhForwardArgs(C.Structure):
     _fields_ = [
         ("n", C.c_int), ("total_len", C.c_int), ("x", vp), ("timesteps", vp), ("duration", vp),
@@ -85,6 +98,9 @@ SIGNATURES = {
                                 C.c_int, C.c_int, C.c_int, vp]),
     "dfh_gemm_w8a8_ws": (C.c_int, [vp, C.c_long, vp, C.c_long, vp, C.c_long, vp, vp, vp, C.c_int, C.c_int,
                                 C.c_int, C.c_int, C.c_int, vp, C.c_long, vp]),
+    "dfh_store_kvcache": (C.c_int, [vp, C.c_long, vp, C.c_long, vp, vp, vp, C.c_int, C.c_int, vp]),
+    "dfh_paged_attention_workspace": (C.c_long, [C.POINTER(DfhPagedAttnArgs)]),
+    "dfh_paged_attention": (C.c_int, [C.POINTER(DfhPagedAttnArgs), vp]),
     "dfh_kvcache_create": (C.c_int, [vp, C.c_int, C.c_int, C.c_int, C.POINTER(vp)]),
     "dfh_kvcache_destroy": (C.c_int, [vp]),
     "dfh_kvcache_reset": (C.c_int, [vp, vp]),

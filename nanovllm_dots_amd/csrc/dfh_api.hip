@@ -736,6 +736,67 @@ int dfh_gemm_bf16_ws(const void* A, long lda, const void* B, long ldb, void* C, 
   return 0;
 }
 
+int dfh_store_kvcache(const void* key, long key_stride, const void* value, long value_stride, void* k_cache,
+                      void* v_cache, const int* slot_mapping, int n_tokens, int D, void* stream) {
+  if (n_tokens < 0 || D <= 0) return fail("dfh_store_kvcache: bad shape n=%d D=%d", n_tokens, D);
+  if (n_tokens == 0) return 0;
+  if (!key || !value || !k_cache || !v_cache || !slot_mapping) return fail("dfh_store_kvcache: NULL pointer");
+  if (D % 8 || key_stride % 8 || value_stride % 8 || key_stride < D || value_stride < D)
+    return fail("dfh_store_kvcache: D and strides must be multiples of 8 (strides >= D)");
+  if (((uintptr_t)key | (uintptr_t)value | (uintptr_t)k_cache | (uintptr_t)v_cache) & 15)
+    return fail("dfh_store_kvcache: buffers must be 16-byte aligned");
+  DFH_CHECK(dfh::store_kvcache(static_cast<const uint16_t*>(key), key_stride, static_cast<const uint16_t*>(value),
+                               value_stride, static_cast<uint16_t*>(k_cache), static_cast<uint16_t*>(v_cache),
+                               slot_mapping, n_tokens, D, reinterpret_cast<hipStream_t>(stream)));
+  return 0;
+}
+
+long dfh_paged_attention_workspace(const DfhPagedAttnArgs* a) {
+  if (!a || a->batch <= 0 || a->num_kv_heads <= 0 || a->num_heads % a->num_kv_heads || a->max_seqlen_q <= 0 ||
+      a->max_seqlen_k <= 0)
+    return 0;
+  return 4 * dfh::paged_attention_ws_floats(a->batch, a->num_kv_heads, a->num_heads / a->num_kv_heads,
+                                            a->max_seqlen_q, a->max_seqlen_k, a->head_dim);
+}
+
+int dfh_paged_attention(const DfhPagedAttnArgs* a, void* stream) {
+  if (!a) return fail("null argument");
+  if (a->batch <= 0 || a->num_heads <= 0 || a->num_kv_heads <= 0 || a->num_heads % a->num_kv_heads)
+    return fail("dfh_paged_attention: bad heads (batch=%d heads=%d kv_heads=%d)", a->batch, a->num_heads,
+                a->num_kv_heads);
+  if (a->head_dim != 64 && a->head_dim != 128)
+    return fail("dfh_paged_attention: head_dim %d not supported (64 or 128)", a->head_dim);
+  if (a->max_seqlen_q <= 0 || a->max_seqlen_k <= 0)
+    return fail("dfh_paged_attention: max_seqlen_q / max_seqlen_k must be positive");
+  if (!a->q || !a->k || !a->v || !a->out || !a->cu_seqlens_q || !a->workspace)
+    return fail("dfh_paged_attention: a required pointer is NULL");
+  if (!a->cu_seqlens_k && !(a->seqlens_k && a->block_table))
+    return fail("dfh_paged_attention: key lengths need cu_seqlens_k (or seqlens_k with a block table)");
+  if (a->block_table && (a->block_size <= 0 || a->block_size % 256 || a->block_table_stride <= 0))
+    return fail("dfh_paged_attention: block_size %d must be a positive multiple of 256", a->block_size);
+  const long D = (long)a->num_kv_heads * a->head_dim;
+  if (a->q_stride < (long)a->num_heads * a->head_dim || a->kv_stride < D || a->q_stride % 8 || a->kv_stride % 8 ||
+      a->out_stride < (long)a->num_heads * a->head_dim)
+    return fail("dfh_paged_attention: bad strides");
+  if (((uintptr_t)a->q | (uintptr_t)a->k | (uintptr_t)a->v) & 15)
+    return fail("dfh_paged_attention: q, k, v must be 16-byte aligned");
+  const long need = dfh_paged_attention_workspace(a);
+  if (a->workspace_bytes < need)
+    return fail("dfh_paged_attention: workspace %ld bytes < %ld needed", a->workspace_bytes, need);
+  dfh::PagedAttnArgs x{};
+  x.batch = a->batch; x.heads = a->num_heads; x.kv_heads = a->num_kv_heads; x.head_dim = a->head_dim;
+  x.max_q = a->max_seqlen_q; x.max_k = a->max_seqlen_k;
+  x.q = static_cast<const uint16_t*>(a->q); x.q_stride = a->q_stride; x.cu_q = a->cu_seqlens_q;
+  x.k = static_cast<const uint16_t*>(a->k); x.v = static_cast<const uint16_t*>(a->v); x.kv_stride = a->kv_stride;
+  x.cu_k = a->cu_seqlens_k; x.seqlens_k = a->seqlens_k;
+  x.block_table = a->block_table; x.bt_stride = a->block_table_stride; x.block_size = a->block_size;
+  x.out = static_cast<uint16_t*>(a->out); x.out_stride = a->out_stride;
+  x.scale = a->softmax_scale; x.causal = a->causal;
+  x.ws = static_cast<float*>(a->workspace);
+  DFH_CHECK(dfh::paged_attention(x, reinterpret_cast<hipStream_t>(stream)));
+  return 0;
+}
+
 int dfh_quant_act_i8(const void* x, long ldx, void* q, long ldq, void* scale, int M, int K, void* stream) {
   if (!x || !q || !scale) return fail("dfh_quant_act_i8: NULL pointer");
   if (M < 0 || K <= 0 || K % 8 || ldx % 8 || ldq % 8 || ldx < K || ldq < K)

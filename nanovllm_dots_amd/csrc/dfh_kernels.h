@@ -118,6 +118,33 @@ hipError_t decode_attention(const uint16_t* qk, long ldqk, const uint16_t* vt, l
                             long ldo, const AttnSeq* seqs, int n_seq, int heads, int max_kv,
                             float* part, hipStream_t s);
 
+// Paged attention of appended tokens over a paged (or contiguous) KV cache
+// (flash_attn_varlen_func / flash_attn_with_kvcache semantics, bottom-right
+// causal, GQA). head_dim 64 or 128; block_size a multiple of 256 when paged.
+struct PagedAttnArgs {
+  int batch, heads, kv_heads, head_dim, max_q, max_k;
+  const uint16_t* q;
+  long q_stride;                 // elements between query tokens
+  const int* cu_q;               // [batch + 1]
+  const uint16_t* k;
+  const uint16_t* v;
+  long kv_stride;                // elements between key tokens
+  const int* cu_k;               // [batch + 1] or null (then seqlens_k)
+  const int* seqlens_k;          // [batch] or null
+  const int* block_table;        // [batch, bt_stride] or null (contiguous K / V at rows cu_k[i] + t)
+  int bt_stride, block_size;
+  uint16_t* out;
+  long out_stride;
+  float scale;
+  int causal;
+  float* ws;                     // paged_attention_ws_floats(...) floats
+};
+long paged_attention_ws_floats(int batch, int kv_heads, int group, int max_q, int max_k, int head_dim);
+hipError_t paged_attention(const PagedAttnArgs& a, hipStream_t s);
+// key / value [n, D] rows (strides in elements) -> cache rows slots[i] ([num_slots, D]); slot < 0 skips
+hipError_t store_kvcache(const uint16_t* key, long key_stride, const uint16_t* value, long value_stride,
+                         uint16_t* k_cache, uint16_t* v_cache, const int* slots, int n, int D, hipStream_t s);
+
 }  // namespace dfh
 
 #include <hip/hip_ext.h>
