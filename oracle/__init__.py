@@ -13,4 +13,6 @@ Modules:
              the int32-accumulate linear.
   kvcache_ref  per-(timestep, layer) prefix K/V cache semantics for a
              MeanFlow solve (extend + active passes).
+  paged_attn_ref  the LLM backbone's paged KV cache: store_kvcache and the
+             varlen / paged attention (bottom-right causal, GQA) in float64.
 """
