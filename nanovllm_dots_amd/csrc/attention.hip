@@ -12,13 +12,14 @@
 // softmax(q k^T / 8) v with an online (flash) softmax.
 //
 // Work split: one workgroup = 128 query rows of one (sequence, head); wave w
-// owns 32 of them. A work list (one item per existing 128-query tile, longest
-// tiles first) is built once per pass; workgroup v takes item v / heads, head
-// v % heads, so the dispatcher hands out the longest tiles first and no
-// workgroup is dispatched for a tile that does not exist before all real ones.
-// Workgroup v runs on XCD v % 8; with heads a multiple of 8 every query tile of
-// one (sequence, head) runs on the same XCD, whose L2 then serves their shared
-// K/V tiles.
+// owns 32 of them. A work list (one item per existing 128-query tile: the
+// sequences with the most tiles first, each sequence's tiles together, longest
+// first) is built once per pass; workgroup v takes item v / heads, head
+// v % heads, so the dispatcher hands out long tiles early and no workgroup is
+// dispatched for a tile that does not exist before all real ones. Workgroup v
+// runs on XCD v % 8; with heads a multiple of 8 every query tile of one
+// (sequence, head) runs on the same XCD and close in time, so that XCD's L2
+// serves their shared K/V tiles.
 //
 // Per 64-key tile, K and V^T arrive by global->LDS DMA into double-buffered,
 // XOR-swizzled tiles (16-B chunk c of row r at slot c ^ ((r >> 1) & 7), which
@@ -53,32 +54,60 @@ __device__ __forceinline__ int att_off(int r, int c) { return r * 64 + ((c ^ ((r
 // row index with bits 2 and 3 swapped
 __device__ __forceinline__ int key_perm(int x) { return (x & ~12) | ((x & 4) << 1) | ((x & 8) >> 1); }
 
-// One workgroup builds the work list: one item per 128-query tile of every
-// sequence, ordered by tile index, highest first (LDS atomics hand out slots).
+// One workgroup builds the work list: sequences in order of tile count, most
+// first, each sequence's tiles consecutive and longest (highest index) first.
+// The dispatcher then hands out the longest tiles early, the shortest last, and
+// the query tiles of one (sequence, head) run close together in time, so their
+// shared K / V tiles are still in L2. Sequences are bucketed by tile count (the
+// last bucket takes every count from kLevels - 1 up); a suffix scan over the
+// buckets gives each bucket's first item, and LDS atomics hand out places in a
+// bucket.
+constexpr int kLevels = 2048;
+
 __global__ void __launch_bounds__(1024) attention_worklist_kernel(const AttnSeq* __restrict__ seqs, int n_seq,
                                                                   char* __restrict__ list) {
-  __shared__ int s_cnt, s_levels;
+  __shared__ int s_start[kLevels];  // items of bucket b, then its next free item
+  __shared__ int s_part[1024];
   AttnItem* items = reinterpret_cast<AttnItem*>(list + kAttnListHeader);
-  if (threadIdx.x == 0) { s_cnt = 0; s_levels = 0; }
+  const int tid = threadIdx.x;
+  for (int b = tid; b < kLevels; b += 1024) s_start[b] = 0;
   __syncthreads();
-  for (int i = threadIdx.x; i < n_seq; i += blockDim.x)
-    atomicMax(&s_levels, (seqs[i].q_end - seqs[i].q_begin + BQ - 1) / BQ);
+  for (int i = tid; i < n_seq; i += 1024) {
+    const int L = (seqs[i].q_end - seqs[i].q_begin + BQ - 1) / BQ;
+    if (L > 0) atomicAdd(&s_start[min(L, kLevels - 1)], L);
+  }
   __syncthreads();
-  for (int lv = s_levels - 1; lv >= 0; --lv) {
-    for (int i = threadIdx.x; i < n_seq; i += blockDim.x) {
-      const AttnSeq sq = seqs[i];
-      if ((sq.q_end - sq.q_begin + BQ - 1) / BQ > lv) {
-        AttnItem it;
-        it.seq = sq;
-        it.tile = lv;
-#pragma unroll
-        for (int k = 0; k < 7; ++k) it.pad[k] = 0;
-        items[atomicAdd(&s_cnt, 1)] = it;
-      }
-    }
+  // exclusive scan from the highest bucket down: thread t owns buckets
+  // kLevels-1-2t and kLevels-2-2t
+  const int b0 = kLevels - 1 - 2 * tid, b1 = b0 - 1;
+  const int a0 = s_start[b0], a1 = s_start[b1];
+  s_part[tid] = a0 + a1;
+  __syncthreads();
+  for (int o = 1; o < 1024; o <<= 1) {
+    const int add = tid >= o ? s_part[tid - o] : 0;
+    __syncthreads();
+    s_part[tid] += add;
     __syncthreads();
   }
-  if (threadIdx.x == 0) *reinterpret_cast<int*>(list) = s_cnt;
+  const int excl = s_part[tid] - (a0 + a1);
+  s_start[b0] = excl;
+  s_start[b1] = excl + a0;
+  __syncthreads();
+  for (int i = tid; i < n_seq; i += 1024) {
+    const AttnSeq sq = seqs[i];
+    const int L = (sq.q_end - sq.q_begin + BQ - 1) / BQ;
+    if (L <= 0) continue;
+    const int off = atomicAdd(&s_start[min(L, kLevels - 1)], L);
+    for (int k = 0; k < L; ++k) {
+      AttnItem it;
+      it.seq = sq;
+      it.tile = L - 1 - k;
+#pragma unroll
+      for (int q = 0; q < 7; ++q) it.pad[q] = 0;
+      items[off + k] = it;
+    }
+  }
+  if (tid == 0) *reinterpret_cast<int*>(list) = s_part[1023];
 }
 
 __global__ void __launch_bounds__(256, 3)

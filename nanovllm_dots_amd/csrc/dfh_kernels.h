@@ -92,8 +92,9 @@ struct AttnSeq {
 };
 
 // Work list of seq_attention: word 0 the item count, then from byte 64 one
-// AttnItem per 128-query tile of a sequence, longest tiles (the highest tile
-// index of any sequence) first. At most one item per query row, so
+// AttnItem per 128-query tile of a sequence: sequences by tile count, most
+// first, each sequence's tiles together from the highest index (the longest)
+// down. At most one item per query row, so
 // 64 + 64 * (query rows of all sequences) bytes suffice.
 struct AttnItem {
   AttnSeq seq;
