@@ -261,9 +261,9 @@ def main():
                     help="run a device copy of this size first (HBM counter calibration under rocprofv3)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one GPU: the FM head shards requests across GPUs with no "
-              "collective on the hot path, and this build runs on single-GPU boxes only "
-              "(--gpus 1).", file=sys.stderr)
+        print("bench.py measures one GPU (--gpus 1): the FM head would shard requests across "
+              "GPUs with no collective on the hot path, and the multi-GPU path is not built.",
+              file=sys.stderr)
         sys.exit(2)
 
     import torch
