@@ -6,8 +6,11 @@ concurrent requests, context lengths U{64..1024}, 16 latent rows x 64-d each,
 weights N(0, 0.02), contexts N(0,1), noise N(0,1), g_cond = 0.
 
 Prints one JSON line:
-  value        DiT GEMM TFLOP/s = 12 * 2*M*(4H^2 + 2HF) * NFE / wall-per-solve,
-               M = sum(c_i + 16) unpadded rows
+  value        DiT GEMM TFLOP/s = executed GEMM FLOPs per solve / wall-per-solve:
+               NFE * [11 * 2*M*(4H^2 + 2HF) + 2*M*3H^2 + 2*N*P*(H^2 + 2HF)],
+               M = sum(c_i + 16) unpadded rows; the last block's O projection and
+               MLP run on the N*P latent rows only, the rows the caller keeps
+               (reference_equivalent_tflops counts 12 full blocks instead)
   roofline     the dominant GEMM (largest total time) timed with dispatch-packet
                HIP events inside the timed region
   cpu_baseline the oracle's float32 DiT on the host cores over a bounded
@@ -322,10 +325,14 @@ def main():
     log(f"timed: {ms:.3f} ms/solve (host wall {wall / args.steps * 1e3:.3f} ms)")
     assert torch.isfinite(out.float()).all()
 
-    gemm_flops = R.dit_gemm_flops(cfg, M) * 4
+    H, F = cfg.hidden, cfg.ffn
+    ref_gemm_flops = R.dit_gemm_flops(cfg, M) * 4
+    # GEMM FLOPs the solve executes: the last block runs QKV over every row and
+    # the O projection and MLP over the n*P latent rows only (latent tail)
+    NP = n * cfg.patch
+    gemm_flops = 4 * (R.dit_gemm_flops(cfg, M) - M * 2 * (H * H + 2 * H * F) + NP * 2 * (H * H + 2 * H * F))
     tflops = gemm_flops / (ms * 1e-3) / 1e12
     xrt = n * cfg.patch * FRAME_S / (ms * 1e-3)
-    H, F = cfg.hidden, cfg.ffn
     per_launch = {"qkv_gemm": 2 * M * H * 3 * H, "o_gemm": 2 * M * H * H,
                   "fc1_gemm": 2 * M * H * F, "fc2_gemm": 2 * M * F * H}
     # compulsory HBM bytes per launch: A, W, outputs (+ residual read for gate-residual)
@@ -342,6 +349,9 @@ def main():
     breakdown = {k: {"ms_per_solve": v[0] / args.steps, "launches_per_solve": v[1] / args.steps}
                  for k, v in classes.items()}
     gemm_ms = sum(role_ms.values()) / args.steps
+    gemm_flops_big = 4 * (cfg.n_blocks * per_launch["qkv_gemm"]
+                          + (cfg.n_blocks - 1) * (per_launch["o_gemm"] + per_launch["fc1_gemm"]
+                                                  + per_launch["fc2_gemm"]))
     log("per-class ms/solve: " + ", ".join(f"{k}={v['ms_per_solve']:.3f}" for k, v in breakdown.items()))
 
     vl = varlen_bench(mf, hist, noise_d, g_d, out)
@@ -365,8 +375,12 @@ def main():
                    "rotary": cfg.rotary, "qk_norm": cfg.qk_norm, "qkv_bias": cfg.qkv_bias,
                    "tokens_per_step_unpadded": M, "padded_T": T},
         "pct_mfma_peak": round(100 * tflops / PEAK_BF16_TFLOPS, 2),
+        "gemm_flops_per_solve": gemm_flops,
+        "reference_gemm_flops_per_solve": ref_gemm_flops,
+        "reference_equivalent_tflops": round(ref_gemm_flops / (ms * 1e-3) / 1e12, 2),
         "latent_xRT": round(xrt, 1),
-        "gemm_only_tflops": round(gemm_flops / (gemm_ms * 1e-3) / 1e12, 2) if gemm_ms > 0 else None,
+        # the four full-size GEMM classes only (the latent tail's small GEMMs are timed apart)
+        "gemm_only_tflops": (round(gemm_flops_big / (gemm_ms * 1e-3) / 1e12, 2) if gemm_ms > 0 else None),
         "roofline": {"bound": "mfma", "kernel": dom, "achieved": round(achieved, 2),
                      "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": pmc_traffic(dom),

@@ -155,13 +155,22 @@ int dfh_input_status(DfhHandle* h, int* flags, void* stream);
 
 /* Per-kernel-class timing with dispatch-packet events (bench instrumentation).
  * classes: 0 qkv gemm, 1 o_proj gemm, 2 fc1 gemm, 3 fc2 gemm, 4 attention,
- * 5 ln_modulate, 6 other. */
+ * 5 ln_modulate, 6 other, 7 the latent tail of the last block (see
+ * dfh_set_latent_tail). */
 int dfh_profile_enable(DfhHandle* h, int enable);
 /* K-split of each GEMM's last, partial round of tiles (default on): leftover
  * tiles are cut along K over the idle workgroups; the workgroup that completes a
  * tile adds the partial sums. Off: every tile runs whole. No reference counterpart
  * (a scheduling choice of this library; results agree to float32 summation order). */
 int dfh_set_ksplit(DfhHandle* h, int enable);
+/* Latent tail of the MeanFlow solves (default on): the caller keeps only the P
+ * latent rows of each DiT output (batched_fm.py:122-124), so the last block
+ * runs LayerNorm + QKV over every row (the latent rows attend over all K/V) and
+ * attention, O projection, LayerNorm and MLP over the latent rows alone; the
+ * final layer reads them. Off: the last block runs over every row, as the
+ * reference does. Both give the same latents up to float32 summation order.
+ * No reference counterpart (an evaluation-order choice of this library). */
+int dfh_set_latent_tail(DfhHandle* h, int enable);
 int dfh_profile_read(DfhHandle* h, double* ms_per_class, long* launches_per_class, int n_classes);
 
 /* Standalone bf16 GEMM: C[M,N] = A[M,K] B[N,K]^T + bias (bias may be NULL).

@@ -70,7 +70,7 @@ hipError_t dev_alloc(DevBuf& b, size_t bytes) {
 template <typename T>
 T* P(DevBuf& b) { return reinterpret_cast<T*>(b.p); }
 
-enum ProfClass { PC_QKV = 0, PC_O, PC_FC1, PC_FC2, PC_ATTN, PC_LN, PC_OTHER, PC_N };
+enum ProfClass { PC_QKV = 0, PC_O, PC_FC1, PC_FC2, PC_ATTN, PC_LN, PC_OTHER, PC_TAIL, PC_N };
 
 }  // namespace
 
@@ -93,12 +93,14 @@ struct DfhHandle {
   long cap_M = 0, ld_vt = 0;
   DevBuf seq, x, hbuf, qk, attn, ff, vt;
   DevBuf row_req, row_pos, vt_col, cu_rows, cu_vt, hist_len, counts, err, patch_rows, seqs;
+  DevBuf tail_seqs, tail_req;  // last block on the latent rows only: their queries, compact row -> request
   DevBuf rope_cos, rope_sin;
   DevBuf temb_in, t_hid, t_out, d_hid, d_out, cond, cond_act, mod;
   DevBuf z, zp, fin, vel, tvals;
   DevBuf splitws;  // K-split: tile counters, then a 256x256 f32 partial tile per resident workgroup
   DevBuf attq;     // attention work list: item count, then one AttnItem per 128-query tile
   bool ksplit = true;
+  bool latent_tail = true;  // solve: the last block's attention / O / MLP on the latent rows only
 
   // profiling
   bool prof = false;
@@ -220,6 +222,8 @@ int reserve(DfhHandle* h, int n, int T, int S, hipStream_t s) {
   DFH_CHECK(dev_alloc(h->err, 16));
   DFH_CHECK(dev_alloc(h->patch_rows, nn * P * 4));
   DFH_CHECK(dev_alloc(h->seqs, (long)nn * SS * sizeof(AttnSeq)));
+  DFH_CHECK(dev_alloc(h->tail_seqs, (long)nn * sizeof(AttnSeq)));
+  DFH_CHECK(dev_alloc(h->tail_req, (long)nn * P * 4));
   DFH_CHECK(dev_alloc(h->rope_cos, (size_t)TT * 32 * 4));
   DFH_CHECK(dev_alloc(h->rope_sin, (size_t)TT * 32 * 4));
   const long RS = (long)SS > nn ? SS : nn;  // timestep rows: per step (solve) or per request (forward)
@@ -298,7 +302,46 @@ struct Pass {
   bool decode = false;         // split-KV decode attention (<= 32 queries / sequence)
   float* part = nullptr;       // decode partials
   bool kv_only_last = false;   // prefix pass: the last block only has to leave its K/V
+  // Only the latent rows' block output is consumed (FM solve: the caller keeps
+  // v[:, -P:], batched_fm.py:122-124). The last block then runs LN + QKV on
+  // every row (the latent queries attend over every row's K/V) and attention,
+  // O projection, LN and MLP on the n_tail latent rows alone, compacted in
+  // request order into h->hbuf (rows tail_rows[j] of the pass -> row j).
+  bool latent_tail = false;
+  const AttnSeq* tail_seqs = nullptr;  // [n_seq]: the latent queries, output row j
+  const int* tail_rows = nullptr;      // [n_tail]: pass row of compact row j
+  const int* tail_req = nullptr;       // [n_tail]: request of compact row j
+  int n_tail = 0;
 };
+
+// The last block on the latent rows only (Pass::latent_tail), after its QKV
+// GEMM over every row. Per row the same operations as the full block; rows
+// that no output depends on are not computed.
+int run_latent_tail(DfhHandle* h, const Pass& p, int l, const uint16_t* ml, long ldm, hipStream_t s) {
+  const DfhConfig& c = h->cfg;
+  const int H = c.hidden, F = c.ffn, NT = p.n_tail;
+  uint16_t* xl = P<uint16_t>(h->hbuf);  // compact residual rows (hbuf's LN output is consumed)
+  uint16_t* hl = P<uint16_t>(h->x);     // compact LN output (x is dead once gathered)
+  uint16_t* al = P<uint16_t>(h->attn);  // compact attention output
+  DFH_CHECK(gather_rows(P<uint16_t>(h->x), p.tail_rows, nullptr, NT, H, xl, s));
+  prof_arm(h, PC_TAIL);
+  DFH_CHECK(attention_worklist(p.tail_seqs, p.n_seq, h->attq.p, s));
+  prof_arm(h, PC_TAIL);
+  DFH_CHECK(seq_attention(p.qk[l], p.ldqk, p.vt[l], p.ld_vt, al, H, c.heads, h->attq.p,
+                          (long)p.n_seq * ((c.patch + 127) / 128), s));
+  GemmArgs o = linear_args(al, H, h->o_w[l], h->o_b[l], xl, H, NT, nullptr, H, H);
+  o.gate = ml + 2 * H; o.ld_gate = ldm; o.row_req = p.tail_req;
+  DFH_CHECK(gemm(h, PC_TAIL, o, EPI_GATE_RES, s));
+  prof_arm(h, PC_TAIL);
+  DFH_CHECK(ln_modulate(xl, H, hl, H, ml + 3 * H, ml + 4 * H, ldm, p.tail_req, nullptr, NT, nullptr, H,
+                        c.ln_eps, s));
+  DFH_CHECK(gemm(h, PC_TAIL, linear_args(hl, H, h->fc1_w[l], h->fc1_b[l], P<uint16_t>(h->ff), F, NT, nullptr,
+                                         F, H), EPI_GELU, s));
+  GemmArgs f2 = linear_args(P<uint16_t>(h->ff), F, h->fc2_w[l], h->fc2_b[l], xl, H, NT, nullptr, H, F);
+  f2.gate = ml + 5 * H; f2.ld_gate = ldm; f2.row_req = p.tail_req;
+  DFH_CHECK(gemm(h, PC_TAIL, f2, EPI_GATE_RES, s));
+  return 0;
+}
 
 int run_blocks(DfhHandle* h, const Pass& p, hipStream_t s) {
   const DfhConfig& c = h->cfg;
@@ -331,6 +374,7 @@ int run_blocks(DfhHandle* h, const Pass& p, hipStream_t s) {
     q.vt = p.vt[l]; q.ld_vt = p.ld_vt; q.vt_col = p.vt_col; q.c_rows = p.c_rows;
     DFH_CHECK(gemm(h, PC_QKV, q, EPI_QKV, s, tile_for(Mup, 3 * H, H, kRoleQKV)));
     if (p.kv_only_last && l == c.n_blocks - 1) break;
+    if (p.latent_tail && l == c.n_blocks - 1) return run_latent_tail(h, p, l, ml, ldm, s);
     prof_arm(h, PC_ATTN);
     if (p.decode)
       DFH_CHECK(decode_attention(p.qk[l], p.ldqk, p.vt[l], p.ld_vt, P<uint16_t>(h->attn), H, p.seqs, p.n_seq,
@@ -358,7 +402,7 @@ int run_blocks(DfhHandle* h, const Pass& p, hipStream_t s) {
 
 // The FM pass over the packed requests of layout(): rows m of h->seq, request
 // row_req[m], q|k into the workspace, V^T in h->vt.
-int dit_blocks(DfhHandle* h, int n, int T, long mod_row0, hipStream_t s) {
+int dit_blocks(DfhHandle* h, int n, int T, long mod_row0, hipStream_t s, bool latent_tail = false) {
   const DfhConfig& c = h->cfg;
   Pass p;
   p.Mup = n * T;
@@ -374,6 +418,13 @@ int dit_blocks(DfhHandle* h, int n, int T, long mod_row0, hipStream_t s) {
   p.seqs = P<AttnSeq>(h->seqs);
   p.n_seq = n;
   p.max_q = T;
+  if (latent_tail) {
+    p.latent_tail = true;
+    p.tail_seqs = P<AttnSeq>(h->tail_seqs);
+    p.tail_rows = P<int>(h->patch_rows);
+    p.tail_req = P<int>(h->tail_req);
+    p.n_tail = n * c.patch;
+  }
   return run_blocks(h, p, s);
 }
 
@@ -384,7 +435,7 @@ int layout(DfhHandle* h, int n, int T, const void* pos_ids, const void* inp, hip
   const DfhConfig& c = h->cfg;
   DFH_CHECK(fm_layout(reinterpret_cast<const float*>(pos_ids), lens, n, T, c.patch, P<int>(h->cu_rows),
                       P<int>(h->cu_vt), P<int>(h->hist_len), P<int>(h->counts), P<int>(h->err),
-                      P<AttnSeq>(h->seqs), s));
+                      P<AttnSeq>(h->seqs), P<AttnSeq>(h->tail_seqs), P<int>(h->tail_req), s));
   DFH_CHECK(fm_gather(reinterpret_cast<const uint16_t*>(inp), src_rows, src_stride, n, T, c.patch, c.hidden,
                       P<int>(h->cu_rows), P<int>(h->cu_vt), P<int>(h->hist_len), P<uint16_t>(h->seq),
                       P<int>(h->row_req), P<int>(h->row_pos), P<int>(h->vt_col),
@@ -413,12 +464,17 @@ int solve_steps(DfhHandle* h, int n, int T, int S, const void* g_cond, const voi
     DFH_CHECK(gemm(h, PC_OTHER, linear_args(P<uint16_t>(h->z), ld, h->coord_w, h->coord_b,
                                             P<uint16_t>(h->zp), H, NP, nullptr, H, ld), EPI_BIAS, s));
     DFH_CHECK(scatter_rows(P<uint16_t>(h->zp), P<int>(h->patch_rows), NP, H, P<uint16_t>(h->seq), s));
-    if (dit_blocks(h, n, T, (long)st * n, s)) return 1;
-    // FinalLayer on the latent rows only
+    const bool tail = h->latent_tail;
+    if (dit_blocks(h, n, T, (long)st * n, s, tail)) return 1;
+    // FinalLayer on the latent rows only (compact in h->hbuf after a latent tail)
     const uint16_t* mf = P<uint16_t>(h->mod) + (long)st * n * h->ld_mod + (long)c.n_blocks * 6 * H;
-    prof_arm(h, PC_LN);
-    DFH_CHECK(ln_modulate(P<uint16_t>(h->x), H, P<uint16_t>(h->fin), H, mf, mf + H, h->ld_mod,
-                          P<int>(h->row_req), P<int>(h->patch_rows), NP, nullptr, H, c.ln_eps, s));
+    prof_arm(h, tail ? PC_TAIL : PC_LN);
+    if (tail)
+      DFH_CHECK(ln_modulate(P<uint16_t>(h->hbuf), H, P<uint16_t>(h->fin), H, mf, mf + H, h->ld_mod,
+                            P<int>(h->tail_req), nullptr, NP, nullptr, H, c.ln_eps, s));
+    else
+      DFH_CHECK(ln_modulate(P<uint16_t>(h->x), H, P<uint16_t>(h->fin), H, mf, mf + H, h->ld_mod,
+                            P<int>(h->row_req), P<int>(h->patch_rows), NP, nullptr, H, c.ln_eps, s));
     DFH_CHECK(gemm(h, PC_OTHER, linear_args(P<uint16_t>(h->fin), H, h->fin_w, h->fin_b,
                                             P<uint16_t>(h->vel), ld, NP, nullptr, ld, H), EPI_BIAS, s));
     DFH_CHECK(z_update(P<uint16_t>(h->z), P<uint16_t>(h->vel), dt_grid[st], (long)NP * ld, s));
@@ -677,6 +733,12 @@ int dfh_input_status(DfhHandle* h, int* flags, void* stream) {
 int dfh_set_ksplit(DfhHandle* h, int enable) {
   if (!h) return fail("null handle");
   h->ksplit = enable != 0;
+  return 0;
+}
+
+int dfh_set_latent_tail(DfhHandle* h, int enable) {
+  if (!h) return fail("null handle");
+  h->latent_tail = enable != 0;
   return 0;
 }
 

@@ -12,9 +12,12 @@ struct TimeVals {
   float v[kMaxTimeVals];
 };
 
-// Request layout from pos_ids (padded inputs) or from lens (varlen inputs)
+// Request layout from pos_ids (padded inputs) or from lens (varlen inputs).
+// Optional: tail_seqs [n] (the P latent queries of each request, output rows
+// i*P + j) and tail_req [n*P] (request of compact latent row i*P + j).
 hipError_t fm_layout(const float* pos_ids, const int* lens, int n, int T, int P, int* cu_rows, int* cu_vt,
-                     int* hist_len, int* counts, int* err, AttnSeq* seqs, hipStream_t s);
+                     int* hist_len, int* counts, int* err, AttnSeq* seqs, AttnSeq* tail_seqs, int* tail_req,
+                     hipStream_t s);
 hipError_t prefix_tables(const uint16_t* rows_in, long stride_in, int m_max, int H, const int* counts,
                          const int* lens, const int* offs, int n, int S, int cap, uint16_t* seq, int* row_req,
                          int* row_pos, int* c_rows, int* vt_col, AttnSeq* seqs, hipStream_t s);
@@ -38,6 +41,7 @@ hipError_t unpack_rows(const uint16_t* src, int n, int T, int P, int D, const in
                        const int* hist_len, uint16_t* dst, hipStream_t s);
 hipError_t scatter_rows(const uint16_t* src, const int* rows_idx, int rows, int H, uint16_t* dst,
                         hipStream_t s);
+// dst row (dst_rows ? dst_rows[r] : r) = src row (src_rows ? src_rows[r] : r), r < rows
 hipError_t gather_rows(const uint16_t* src, const int* src_rows, const int* dst_rows, int rows, int H,
                        uint16_t* dst, hipStream_t s);
 hipError_t z_update(uint16_t* z, const uint16_t* v, float dt, long n, hipStream_t s);

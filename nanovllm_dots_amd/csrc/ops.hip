@@ -93,7 +93,8 @@ ln_modulate_kernel(const uint16_t* __restrict__ x, long ldx, uint16_t* __restric
 __global__ void __launch_bounds__(1024)
 fm_layout_kernel(const float* __restrict__ pos_ids, const int* __restrict__ lens, int n, int T, int P,
                  int* __restrict__ cu_rows, int* __restrict__ cu_vt, int* __restrict__ hist_len,
-                 int* __restrict__ counts, int* __restrict__ err, AttnSeq* __restrict__ seqs) {
+                 int* __restrict__ counts, int* __restrict__ err, AttnSeq* __restrict__ seqs,
+                 AttnSeq* __restrict__ tail_seqs, int* __restrict__ tail_req) {
   __shared__ int s_rows[1024], s_vt[1024];
   const int i = threadIdx.x;
   int c = 0;
@@ -132,6 +133,11 @@ fm_layout_kernel(const float* __restrict__ pos_ids, const int* __restrict__ lens
     // request i: rows [r0, r0 + c + P); history causal below c - 1
     const int r0 = s_rows[i] - Ti, v0 = s_vt[i] - ((Ti + 7) & ~7);
     seqs[i] = AttnSeq{r0, r0, v0, 0, Ti, c - 1, Ti, r0};
+    // the P latent queries alone, output to compact rows i*P .. i*P + P - 1; and
+    // the request of each compact row
+    if (tail_seqs) tail_seqs[i] = AttnSeq{r0, r0, v0, c, Ti, c - 1, Ti, i * P - c};
+    if (tail_req)
+      for (int j = 0; j < P; ++j) tail_req[i * P + j] = i;
   }
   if (i == 0) {
     cu_rows[0] = 0;
@@ -268,7 +274,7 @@ __global__ void gather_rows_kernel(const uint16_t* __restrict__ src, const int* 
   const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (r >= rows) return;
   const uint16_t* sp = src + (long)(src_rows ? src_rows[r] : r) * H;
-  uint16_t* dp = dst + (long)dst_rows[r] * H;
+  uint16_t* dp = dst + (long)(dst_rows ? dst_rows[r] : r) * H;
   for (int col = lane * 8; col < H; col += 64 * 8)
     *reinterpret_cast<uint4*>(dp + col) = *reinterpret_cast<const uint4*>(sp + col);
 }
@@ -400,10 +406,11 @@ hipError_t ln_modulate(const uint16_t* x, long ldx, uint16_t* out, long ldo, con
 }
 
 hipError_t fm_layout(const float* pos_ids, const int* lens, int n, int T, int P, int* cu_rows, int* cu_vt,
-                     int* hist_len, int* counts, int* err, AttnSeq* seqs, hipStream_t s) {
+                     int* hist_len, int* counts, int* err, AttnSeq* seqs, AttnSeq* tail_seqs, int* tail_req,
+                     hipStream_t s) {
   if (n <= 0 || n > 1024 || (!pos_ids && !lens)) return hipErrorInvalidValue;
   hipLaunchKernelGGL(fm_layout_kernel, dim3(1), dim3(1024), 0, s, pos_ids, lens, n, T, P, cu_rows, cu_vt,
-                     hist_len, counts, err, seqs);
+                     hist_len, counts, err, seqs, tail_seqs, tail_req);
   return hipGetLastError();
 }
 

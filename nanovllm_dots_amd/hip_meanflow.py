@@ -277,10 +277,17 @@ class HipFMHead:
         """K-split of each GEMM's last partial round of tiles (on by default)."""
         _lib.check(self.lib.dfh_set_ksplit(self.handle, int(enable)), "dfh_set_ksplit")
 
+    def set_latent_tail(self, enable: bool) -> None:
+        """Last block of a solve on the latent rows only (on by default): the
+        caller keeps v[:, -P:] (batched_fm.py:122-124), so only those rows'
+        attention, O projection and MLP are computed there."""
+        _lib.check(self.lib.dfh_set_latent_tail(self.handle, int(enable)), "dfh_set_latent_tail")
+
     def profile(self, enable: bool) -> None:
         _lib.check(self.lib.dfh_profile_enable(self.handle, int(enable)), "dfh_profile_enable")
 
-    PROFILE_CLASSES = ("qkv_gemm", "o_gemm", "fc1_gemm", "fc2_gemm", "attention", "ln_modulate", "other")
+    PROFILE_CLASSES = ("qkv_gemm", "o_gemm", "fc1_gemm", "fc2_gemm", "attention", "ln_modulate", "other",
+                       "latent_tail")
 
     def profile_read(self) -> dict[str, tuple[float, int]]:
         k = len(self.PROFILE_CLASSES)

@@ -2,6 +2,7 @@
 
     python -m nanovllm_dots_amd.prof_summary stats <run_kernel_stats.csv>
     python -m nanovllm_dots_amd.prof_summary pmc <fetch counter csv> <write counter csv> --calib-mib 256
+    python -m nanovllm_dots_amd.prof_summary mfma <counter csv> [--simds 1024]
 
 ``stats`` tabulates ``rocprofv3 --kernel-trace --stats`` per kernel, with the
 role each GEMM instantiation plays in a DiT block. ``pmc`` reads one
@@ -110,6 +111,70 @@ def pmc_table(factors, out, roles_wanted=("qkv_gemm", "o_gemm", "fc1_gemm", "fc2
     return "\n".join(lines), machine
 
 
+# SQ counters are summed over shader engines and XCDs; GRBM_GUI_ACTIVE is summed over the XCDs
+MFMA_COUNTERS = ("GRBM_GUI_ACTIVE", "SQ_VALU_MFMA_BUSY_CYCLES", "SQ_INSTS_VALU_MFMA_MOPS_BF16", "SQ_INSTS_MFMA",
+                 "SQ_INSTS_VALU", "SQ_ACTIVE_INST_VALU", "SQ_BUSY_CU_CYCLES", "SQ_INSTS_VALU_TRANS_F32")
+
+
+def mfma(path: str, simds: int = 1024, xcds: int = 8):
+    """Per-role medians of one multi-counter ``--pmc`` run.
+
+    mfma_util = SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE per XCD * SIMDs), the
+    expression of rocprofv3's derived ``MfmaUtil``; clock = GRBM_GUI_ACTIVE per XCD /
+    dispatch duration; bf16 MFMA FLOP = SQ_INSTS_VALU_MFMA_MOPS_BF16 * 512.
+    """
+    per = collections.defaultdict(dict)
+    meta = {}
+    for r in csv.DictReader(open(path)):
+        d = int(r["Dispatch_Id"])
+        per[d][r["Counter_Name"]] = per[d].get(r["Counter_Name"], 0.0) + float(r["Counter_Value"])
+        dur = None
+        if r.get("Start_Timestamp") and r.get("End_Timestamp"):
+            dur = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) * 1e-9
+        meta[d] = (r["Kernel_Name"], dur, r.get("Arch_VGPR_Count") or r.get("VGPR_Count"),
+                   r.get("Accum_VGPR_Count"))
+    ids = sorted(per)
+    rl = roles([meta[d][0] for d in ids])
+    by = collections.defaultdict(list)
+    for role, d in zip(rl, ids):
+        c = per[d]
+        gui = c.get("GRBM_GUI_ACTIVE", 0.0) / xcds
+        if gui <= 0:
+            continue
+        name, dur, vg, ag = meta[d]
+        row = {
+            "cycles": gui,
+            "mfma_util": c.get("SQ_VALU_MFMA_BUSY_CYCLES", 0.0) / (gui * simds),
+            "mfma_flop": c.get("SQ_INSTS_VALU_MFMA_MOPS_BF16", 0.0) * 512,
+            "mfma_insts": c.get("SQ_INSTS_MFMA", 0.0),
+            "valu_insts": c.get("SQ_INSTS_VALU", 0.0),
+            "trans_insts": c.get("SQ_INSTS_VALU_TRANS_F32", 0.0),
+            # quad-cycles summed over the SIMDs -> fraction of SIMD cycles with a VALU op in flight
+            "valu_busy": c.get("SQ_ACTIVE_INST_VALU", 0.0) * 4 / (gui * simds),
+            "cu_busy": c.get("SQ_BUSY_CU_CYCLES", 0.0) * 4 / (gui * simds / 4),
+            "clock_ghz": gui / dur / 1e9 if dur else float("nan"),
+            "vgpr": vg, "agpr": ag,
+        }
+        by[role].append(row)
+    return by
+
+
+def mfma_table(by, roles_wanted=("qkv_gemm", "o_gemm", "fc1_gemm", "fc2_gemm", "attention", "ln_modulate")) -> str:
+    lines = ["| role | dispatches | cycles (per XCD) | clock GHz | MFMA busy | bf16 MFMA GFLOP | MFMA insts (M) | "
+             "VALU insts (M) | of which transc. (M) | VALU busy | VGPR / AGPR |",
+             "|---|---:|---:|---:|---:|---:|---:|---:|---:|---:|---|"]
+    for role in roles_wanted:
+        rows = by.get(role)
+        if not rows:
+            continue
+        med = lambda k: statistics.median(r[k] for r in rows)
+        lines.append("| %s | %d | %.0f | %.2f | %.1f %% | %.1f | %.2f | %.2f | %.2f | %.1f %% | %s / %s |" % (
+            role, len(rows), med("cycles"), med("clock_ghz"), 100 * med("mfma_util"), med("mfma_flop") / 1e9,
+            med("mfma_insts") / 1e6, med("valu_insts") / 1e6, med("trans_insts") / 1e6, 100 * med("valu_busy"),
+            rows[0]["vgpr"], rows[0]["agpr"]))
+    return "\n".join(lines)
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser()
     sub = ap.add_subparsers(dest="cmd", required=True)
@@ -120,9 +185,14 @@ def main(argv=None):
     p.add_argument("fetch_csv")
     p.add_argument("write_csv")
     p.add_argument("--calib-mib", type=int, required=True)
+    q = sub.add_parser("mfma")
+    q.add_argument("csv")
+    q.add_argument("--simds", type=int, default=1024)
     a = ap.parse_args(argv)
     if a.cmd == "stats":
         print(stats(a.csv, a.top))
+    elif a.cmd == "mfma":
+        print(mfma_table(mfma(a.csv, a.simds)))
     else:
         factors, out = pmc(a.fetch_csv, a.write_csv, a.calib_mib)
         table, machine = pmc_table(factors, out)
