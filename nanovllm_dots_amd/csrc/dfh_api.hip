@@ -224,8 +224,8 @@ int reserve(DfhHandle* h, int n, int T, int S, hipStream_t s) {
   DFH_CHECK(dev_alloc(h->seqs, (long)nn * SS * sizeof(AttnSeq)));
   DFH_CHECK(dev_alloc(h->tail_seqs, (long)nn * sizeof(AttnSeq)));
   DFH_CHECK(dev_alloc(h->tail_req, (long)nn * P * 4));
-  DFH_CHECK(dev_alloc(h->rope_cos, (size_t)TT * 32 * 4));
-  DFH_CHECK(dev_alloc(h->rope_sin, (size_t)TT * 32 * 4));
+  DFH_CHECK(dev_alloc(h->rope_cos, (size_t)((TT + 31) / 32) * 32 * 32 * 4));  // whole 32-position groups
+  DFH_CHECK(dev_alloc(h->rope_sin, (size_t)((TT + 31) / 32) * 32 * 32 * 4));
   const long RS = (long)SS > nn ? SS : nn;  // timestep rows: per step (solve) or per request (forward)
   DFH_CHECK(dev_alloc(h->temb_in, RS * c.freq_dim * 2));
   DFH_CHECK(dev_alloc(h->t_hid, RS * H * 2));

@@ -30,6 +30,8 @@ hipError_t cache_advance(int* lens, const int* counts, int n, hipStream_t s);
 hipError_t fm_gather(const uint16_t* inp, const uint16_t* const* src_rows, long src_stride, int n, int T,
                      int P, int H, const int* cu_rows, const int* cu_vt, const int* hist_len, uint16_t* seq,
                      int* row_req, int* row_pos, int* vt_col, int* patch_rows, int* err, hipStream_t s);
+// cos / sin of pos * inv_freq[d] (float32) for half = 32, positions grouped by 32
+// (rope_table_kernel); the tables hold ceil(max_pos / 32) * 32 * 32 floats
 hipError_t rope_table(const float* inv_freq, int half, int max_pos, float* cosv, float* sinv,
                       hipStream_t s);
 hipError_t timestep_embed(const float* tv, const TimeVals& tvh, int rows, const float* freqs, int half,

@@ -362,12 +362,14 @@ __device__ __forceinline__ void qkv_epilogue(const GemmArgs& a, ACC (&acc)[C::RN
         }
       }
       if (a.rope_cos) {
-        const float* cs = a.rope_cos + (long)pos * 32;
-        const float* sn = a.rope_sin + (long)pos * 32;
+        // tables grouped by 32 positions (rope_table): this lane's d = 8g + 4hi + t
+        const long to = ((long)(pos >> 5) * 256 + (pos & 31) * 2 + hi) * 4;
+        const float* cs = a.rope_cos + to;
+        const float* sn = a.rope_sin + to;
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
-          const int d = 8 * (v >> 2) + 4 * hi + (v & 3);
-          const float c = cs[d], s = sn[d];
+          const int tg = (v >> 2) * 256 + (v & 3);
+          const float c = cs[tg], s = sn[tg];
           const float r0 = add_rn(mul_rn(x0[v], c), mul_rn(-x1[v], s));
           const float r1 = add_rn(mul_rn(x1[v], c), mul_rn(x0[v], s));
           x0[v] = r0;

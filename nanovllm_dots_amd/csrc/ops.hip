@@ -204,14 +204,21 @@ __global__ void unpack_rows_kernel(const uint16_t* __restrict__ src, int n, int 
 }
 
 // RoPE tables: cos/sin of pos * inv_freq[d] in fp32 (native/layers.py:124-134), [max_pos, hd/2]
+// Layout (half = 32): groups of 32 positions; within a group, for each
+// g = d / 8, the 32 positions' pairs of 16-B chunks (d % 8 < 4, d % 8 >= 4):
+// float index (((p / 32) * 4 + g) * 64 + (p % 32) * 2 + (d / 4) % 2) * 4 + d % 4.
+// The QKV epilogue's lane (row p, half hi) needs d = 8g + 4hi + [0, 4), so a
+// wave's load of one g over 32 consecutive positions reads 1 KB in one or two
+// contiguous pieces.
 __global__ void rope_table_kernel(const float* __restrict__ inv_freq, int half, int max_pos,
                                   float* __restrict__ cosv, float* __restrict__ sinv) {
   const int idx = blockIdx.x * blockDim.x + threadIdx.x;
   if (idx >= max_pos * half) return;
   const int p = idx / half, d = idx % half;
   const float f = mul_rn((float)p, inv_freq[d]);
-  cosv[idx] = cosf(f);
-  sinv[idx] = sinf(f);
+  const long o = ((long)((p >> 5) * 4 + (d >> 3)) * 64 + (p & 31) * 2 + ((d >> 2) & 1)) * 4 + (d & 3);
+  cosv[o] = cosf(f);
+  sinv[o] = sinf(f);
 }
 
 // Sinusoidal timestep embedding (native/dit.py:34-43): row r has value tv[r];
@@ -428,6 +435,7 @@ hipError_t fm_gather(const uint16_t* inp, const uint16_t* const* src_rows, long 
 
 hipError_t rope_table(const float* inv_freq, int half, int max_pos, float* cosv, float* sinv,
                       hipStream_t s) {
+  if (half != 32 || max_pos <= 0) return hipErrorInvalidValue;  // the grouped layout is for head_dim 64
   const int n = half * max_pos;
   hipLaunchKernelGGL(rope_table_kernel, dim3((n + 255) / 256), dim3(256), 0, s, inv_freq, half,
                      max_pos, cosv, sinv);
