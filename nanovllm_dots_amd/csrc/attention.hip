@@ -406,29 +406,69 @@ decode_attention_kernel(const uint16_t* __restrict__ qk, long ldqk, const uint16
   }
 }
 
+// Merge of the chunk partials: one workgroup per (sequence, head, group of
+// DQG queries). Per block of up to DCB chunks, the chunk weights
+// exp2(m_c - M) / L of the group's queries go to LDS; then every thread adds
+// two output columns of one query over the block's chunks with independent
+// loads (64 threads per query read its 256-B O rows coalesced).
+constexpr int DQG = 8;    // queries per combine workgroup
+constexpr int DCB = 256;  // chunks per LDS block of weights
+
 __global__ void __launch_bounds__(256)
 decode_combine_kernel(const float* __restrict__ part, const AttnSeq* __restrict__ seqs, int heads,
                       int n_chunks, uint16_t* __restrict__ out, long ldo) {
+  __shared__ float Ws[DQG][DCB];
+  __shared__ float Mq[DQG], Lq[DQG];
   const AttnSeq sq = seqs[blockIdx.y];
-  const int h = blockIdx.x;
+  const int h = blockIdx.x, qg = blockIdx.z * DQG;
   const int nq = sq.q_end - sq.q_begin;
-  const int nc = (sq.kv_len + DCH - 1) / DCH;
+  if (qg >= nq) return;  // uniform
+  const int R = min(DQG, nq - qg);
+  const int nc = min((sq.kv_len + DCH - 1) / DCH, n_chunks);
   const float* pp = part + (long)(blockIdx.y * heads + h) * n_chunks * PART;
-  for (int e = threadIdx.x; e < 32 * HD; e += 256) {
-    const int q = e / HD, d = e % HD;
-    if (q >= nq) continue;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  // row max and sum of each query over all chunks: wave w takes queries w and w + 4
+  for (int r = wave; r < R; r += 4) {
+    const int q = qg + r;
     float M = -INFINITY;
-    for (int c = 0; c < nc; ++c) M = fmaxf(M, pp[c * PART + q]);
-    float L = 0.f, O = 0.f;
-    for (int c = 0; c < nc; ++c) {
-      const float mc = pp[c * PART + q];
-      if (mc == -INFINITY) continue;
-      const float w = exp2f(mc - M);
-      L += pp[c * PART + 32 + q] * w;
-      O += pp[c * PART + 64 + q * HD + d] * w;
-    }
-    out[(long)(sq.out_row0 + sq.q_begin + q) * ldo + h * HD + d] = f2bf(O / L);
+    for (int c = lane; c < nc; c += 64) M = fmaxf(M, pp[(long)c * PART + q]);
+    M = wave_max(M);
+    float L = 0.f;
+    if (M != -INFINITY)
+      for (int c = lane; c < nc; c += 64) {
+        const float mc = pp[(long)c * PART + q];
+        if (mc != -INFINITY) L += pp[(long)c * PART + 32 + q] * exp2f(mc - M);
+      }
+    L = wave_sum(L);
+    if (lane == 0) { Mq[r] = M; Lq[r] = L; }
   }
+  __syncthreads();
+  const int r = tid >> 5, d = (tid & 31) * 2;  // this thread's query and two output columns
+  float o0 = 0.f, o1 = 0.f;
+  for (int c0 = 0; c0 < nc; c0 += DCB) {
+    const int cn = min(DCB, nc - c0);
+    for (int idx = tid; idx < R * cn; idx += 256) {
+      const int rr = idx / cn, cc = idx % cn;
+      const float mc = pp[(long)(c0 + cc) * PART + qg + rr];
+      const float M = Mq[rr], L = Lq[rr];
+      Ws[rr][cc] = (L > 0.f && mc != -INFINITY) ? exp2f(mc - M) / L : 0.f;
+    }
+    __syncthreads();
+    if (r < R) {
+      const float* po = pp + (long)c0 * PART + 64 + (qg + r) * HD + d;
+#pragma unroll 8
+      for (int cc = 0; cc < cn; ++cc) {
+        const float w = Ws[r][cc];
+        const float2 x = *reinterpret_cast<const float2*>(po + (long)cc * PART);
+        o0 += w != 0.f ? w * x.x : 0.f;
+        o1 += w != 0.f ? w * x.y : 0.f;
+      }
+    }
+    __syncthreads();
+  }
+  if (r < R)
+    *reinterpret_cast<uint32_t*>(out + (long)(sq.out_row0 + sq.q_begin + qg + r) * ldo + h * HD + d) =
+        pack2(o0, o1);
 }
 
 }  // namespace
@@ -460,8 +500,8 @@ hipError_t decode_attention(const uint16_t* qk, long ldqk, const uint16_t* vt, l
              seqs, heads, scale_log2, part, n_chunks);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(decode_combine_kernel, dim3(heads, n_seq), dim3(256), 0, s, part, seqs, heads, n_chunks,
-                     out, ldo);
+  hipLaunchKernelGGL(decode_combine_kernel, dim3(heads, n_seq, 32 / DQG), dim3(256), 0, s, part, seqs, heads,
+                     n_chunks, out, ldo);
   return hipGetLastError();
 }
 

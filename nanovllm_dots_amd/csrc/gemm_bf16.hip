@@ -892,13 +892,17 @@ template <class C, class Op, int EPI>
 hipError_t launch(const GemmArgs& a_in, hipStream_t s) {
   auto kern = gemm_mfma_kernel<C, Op, EPI>;
   const long tiles_upper = (long)((a_in.M + C::BM - 1) / C::BM) * (a_in.N / C::BN);
-  long grid = (long)num_cus() * C::WG_PER_CU;
-  if (tiles_upper < grid) grid = ((tiles_upper + 7) / 8) * 8;
-  if (grid < 8) grid = 8;
+  const long full = (long)num_cus() * C::WG_PER_CU;
   GemmArgs a = a_in;
   // the K-split needs the counters and a partial-sum tile per workgroup; QKV keeps whole tiles
-  if (a.ws && (EPI == EPI_QKV || grid > kSplitCounters || a.ws_elems < kSplitCounters + grid * C::BM * C::BN))
+  if (a.ws && (EPI == EPI_QKV || full > kSplitCounters || a.ws_elems < kSplitCounters + full * C::BM * C::BN))
     a.ws = nullptr;
+  // Fewer tiles than resident workgroups: with a workspace the whole grid runs
+  // and the idle workgroups take K pieces of the tiles (the split of a partial
+  // last round, here the only round); without one the grid shrinks to the tiles.
+  long grid = full;
+  if (tiles_upper < grid && !a.ws) grid = ((tiles_upper + 7) / 8) * 8;
+  if (grid < 8) grid = 8;
   dfh_launch(kern, dim3((unsigned)grid), dim3(C::THREADS), 0, s, a);
   return hipGetLastError();
 }

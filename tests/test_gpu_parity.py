@@ -253,6 +253,9 @@ def test_full_size_nfe4_solve():
 
 
 @pytest.mark.parametrize("M,K,N,tile,epi", [(36937, 4096, 1024, 8, 4), (36937, 1024, 4096, 8, 1),
+                                            # fewer tiles than resident workgroups: every tile is split
+                                            (68, 4096, 1024, 3, 4), (68, 1024, 4096, 3, 1), (68, 1024, 1024, 3, 0),
+                                            (1024, 1024, 4096, 2, 4), (1024, 4096, 1024, 3, 4), (5, 4096, 256, 3, 4),
                                             (20000, 1024, 4096, 0, 4), (3000, 2048, 256, 3, 4),
                                             (700, 1024, 256, 3, 0)])
 def test_gemm_ksplit_matches_whole_tiles(M, K, N, tile, epi):
