@@ -312,6 +312,23 @@ decode_attention_kernel(const uint16_t* __restrict__ qk, long ldqk, const uint16
     for (int kk = 0; kk < 4; ++kk) qf[kk] = *reinterpret_cast<const bf16x8*>(qp + 16 * kk);
   }
   const int key0 = k_chunk + wave * 64;
+  // V^T fragments of this wave's 64 keys (columns kc..kc+3 and kc+8..kc+11 of
+  // rows d), requested before the scores so their latency overlaps K's
+  bf16x8 vf[2][2][2];  // [kb][half][db]
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+      const int kc = key0 + kb * 32 + 16 * half + 4 * hi;
+#pragma unroll
+      for (int db = 0; db < 2; ++db) {
+        const uint16_t* vp = vt + (long)(h * HD + db * 32 + l32) * ld_vt + sq.vt_col0 + kc;
+        const uint2 lo = *reinterpret_cast<const uint2*>(vp);
+        const uint2 up = *reinterpret_cast<const uint2*>(vp + 8);
+        uint4 u = make_uint4(lo.x, lo.y, up.x, up.y);
+        vf[kb][half][db] = *reinterpret_cast<bf16x8*>(&u);
+      }
+    }
   floatx16 s[2];
 #pragma unroll
   for (int kb = 0; kb < 2; ++kb) {
@@ -360,16 +377,9 @@ decode_attention_kernel(const uint16_t* __restrict__ qk, long ldqk, const uint16
       bf16x8 pf;
 #pragma unroll
       for (int j = 0; j < 8; ++j) pf[j] = (__bf16)s[kb][8 * half + j];
-      const int kc = key0 + kb * 32 + 16 * half + 4 * hi;  // columns kc..kc+3 and kc+8..kc+11
 #pragma unroll
-      for (int db = 0; db < 2; ++db) {
-        const uint16_t* vp = vt + (long)(h * HD + db * 32 + l32) * ld_vt + sq.vt_col0 + kc;
-        const uint2 lo = *reinterpret_cast<const uint2*>(vp);
-        const uint2 up = *reinterpret_cast<const uint2*>(vp + 8);
-        uint4 u = make_uint4(lo.x, lo.y, up.x, up.y);
-        const bf16x8 vf = *reinterpret_cast<bf16x8*>(&u);
-        o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf, o[db], 0, 0, 0);
-      }
+      for (int db = 0; db < 2; ++db)
+        o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[kb][half][db], pf, o[db], 0, 0, 0);
     }
   // O^T[d][q] in lanes: q = l32, d = db*32 + 8*(v/4) + 4*hi + v%4
 #pragma unroll

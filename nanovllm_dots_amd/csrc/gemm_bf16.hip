@@ -894,8 +894,8 @@ hipError_t launch(const GemmArgs& a_in, hipStream_t s) {
   const long tiles_upper = (long)((a_in.M + C::BM - 1) / C::BM) * (a_in.N / C::BN);
   const long full = (long)num_cus() * C::WG_PER_CU;
   GemmArgs a = a_in;
-  // the K-split needs the counters and a partial-sum tile per workgroup; QKV keeps whole tiles
-  if (a.ws && (EPI == EPI_QKV || full > kSplitCounters || a.ws_elems < kSplitCounters + full * C::BM * C::BN))
+  // the K-split needs the counters and a partial-sum tile per workgroup
+  if (a.ws && (full > kSplitCounters || a.ws_elems < kSplitCounters + full * C::BM * C::BN))
     a.ws = nullptr;
   // Fewer tiles than resident workgroups: with a workspace the whole grid runs
   // and the idle workgroups take K pieces of the tiles (the split of a partial
