@@ -260,6 +260,8 @@ def main():
     ap.add_argument("--no-w8a8", action="store_true")
     ap.add_argument("--no-kvcache", action="store_true")
     ap.add_argument("--no-paged", action="store_true")
+    ap.add_argument("--kvcache-only", action="store_true",
+                    help="run only the KV-cached solve leg (4 streams x 10,111 cached rows) and print its record")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="run a device copy of this size first (HBM counter calibration under rocprofv3)")
     args = ap.parse_args()
@@ -285,6 +287,10 @@ def main():
     cfg = R.DitConfig(hidden=1024, heads=16, ffn=4096, n_blocks=12, latent_dim=64, patch=16)
     log("generating weights / inputs")
     W = R.random_dit_weights(cfg, args.seed)
+    if args.kvcache_only:
+        print(json.dumps({"kvcache_4x10111": kvcache_bench(HipFMHead(FMSpec.of(cfg), W, device=dev), cfg)}),
+              flush=True)
+        return
     lens, hist, noise = R.synthetic_requests(args.requests, 64, 1024, cfg, seed=args.seed,
                                              regime="bf16")
     inp, _, pos, g = R.pack_fm_inputs(hist, cfg.patch, cfg.hidden)
