@@ -281,9 +281,12 @@ seq_attention_kernel(const uint16_t* __restrict__ qk, long ldqk, const uint16_t*
 // Split-KV decode attention for the cached solve: <= 32 queries per sequence,
 // every query sees all kv_len keys (the active rows' mask row in
 // native/model.py:57-75). A workgroup takes DCH keys of one (sequence, head);
-// each wave 64 of them, with K and V^T fragments loaded straight from HBM into
-// MFMA operand registers (each key is used once, so LDS staging buys nothing).
-// The four waves' partial softmax states merge in LDS; chunks merge in
+// each wave 64 of them. Each key is used once, so a wave stages only its own
+// 64-key K and V^T tiles: global->LDS DMA moves whole 128-B lines (8 lines per
+// 1 KB instruction), where direct operand loads would touch 32 lines per
+// instruction and every V^T line eight times. The tiles use the swizzle and
+// the key-row permutation of seq_attention_kernel. The four waves' partial
+// softmax states merge in LDS (over the tiles' space); chunks merge in
 // decode_combine_kernel.
 constexpr int DCH = 256;
 constexpr int PART = 32 * 66;  // per chunk: m[32], l[32], O[32][64]
@@ -292,8 +295,12 @@ __global__ void __launch_bounds__(256)
 decode_attention_kernel(const uint16_t* __restrict__ qk, long ldqk, const uint16_t* __restrict__ vt,
                         long ld_vt, const AttnSeq* __restrict__ seqs, int heads, float scale_log2,
                         float* __restrict__ part, int n_chunks) {
-  __shared__ float Ow[4][HD][33];
+  // per wave: K tile [64 keys][64] then V^T tile [64 d][64 keys], 16 KB; after the
+  // scores and P.V the same space holds the waves' O^T for the merge
+  __shared__ __attribute__((aligned(16))) uint16_t tiles[4 * 2 * BKV * HD];
   __shared__ float Mw[4][32], Lw[4][32];
+  float (*Ow)[HD][33] = reinterpret_cast<float (*)[HD][33]>(tiles);
+  static_assert(sizeof(float) * 4 * HD * 33 <= sizeof(uint16_t) * 4 * 2 * BKV * HD, "merge space");
   const AttnSeq sq = seqs[blockIdx.z];
   const int h = blockIdx.y, chunk = blockIdx.x;
   const int kv = sq.kv_len;
@@ -303,7 +310,22 @@ decode_attention_kernel(const uint16_t* __restrict__ qk, long ldqk, const uint16
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l32 = lane & 31, hi = lane >> 5;
   const int nq = sq.q_end - sq.q_begin;
-
+  const int key0 = k_chunk + wave * BKV;
+  uint16_t* Kw = tiles + wave * 2 * BKV * HD;
+  uint16_t* Vw = Kw + BKV * HD;
+  // DMA: load j fills tile rows [8j, 8j + 8): lane -> row 8j + lane/8, slot lane%8,
+  // which holds source chunk (lane%8) ^ swz(row). K rows past kv_len repeat the
+  // last key (masked below); V^T columns past it are finite (zeroed slack)
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int r = j * 8 + (lane >> 3);
+    const int c = (lane & 7) ^ ((r >> 1) & 7);
+    const int key = min(key0 + r, kv - 1);
+    __builtin_amdgcn_global_load_lds(DFH_GPTR(qk + (long)(sq.kv_row0 + key) * ldqk + H + h * HD + c * 8),
+                                     DFH_LPTR(Kw + j * 8 * HD), 16, 0, 0);
+    __builtin_amdgcn_global_load_lds(DFH_GPTR(vt + (long)(h * HD + r) * ld_vt + sq.vt_col0 + key0 + c * 8),
+                                     DFH_LPTR(Vw + j * 8 * BKV), 16, 0, 0);
+  }
   const int qi = l32 < nq ? l32 : nq - 1;
   bf16x8 qf[4];
   {
@@ -311,44 +333,26 @@ decode_attention_kernel(const uint16_t* __restrict__ qk, long ldqk, const uint16
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) qf[kk] = *reinterpret_cast<const bf16x8*>(qp + 16 * kk);
   }
-  const int key0 = k_chunk + wave * 64;
-  // V^T fragments of this wave's 64 keys (columns kc..kc+3 and kc+8..kc+11 of
-  // rows d), requested before the scores so their latency overlaps K's
-  bf16x8 vf[2][2][2];  // [kb][half][db]
-#pragma unroll
-  for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-    for (int half = 0; half < 2; ++half) {
-      const int kc = key0 + kb * 32 + 16 * half + 4 * hi;
-#pragma unroll
-      for (int db = 0; db < 2; ++db) {
-        const uint16_t* vp = vt + (long)(h * HD + db * 32 + l32) * ld_vt + sq.vt_col0 + kc;
-        const uint2 lo = *reinterpret_cast<const uint2*>(vp);
-        const uint2 up = *reinterpret_cast<const uint2*>(vp + 8);
-        uint4 u = make_uint4(lo.x, lo.y, up.x, up.y);
-        vf[kb][half][db] = *reinterpret_cast<bf16x8*>(&u);
-      }
-    }
+  wait_vm_lgkm0<0>();  // this wave's tiles are in LDS (only this wave reads them)
+  const int krow = key_perm(l32);
   floatx16 s[2];
 #pragma unroll
   for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
     for (int v = 0; v < 16; ++v) s[kb][v] = 0.f;
-    int key = key0 + kb * 32 + l32;
-    key = key < kv ? key : kv - 1;
-    const uint16_t* kp = qk + (long)(sq.kv_row0 + key) * ldqk + H + h * HD + 8 * hi;
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
-      const bf16x8 kf = *reinterpret_cast<const bf16x8*>(kp + 16 * kk);
+      const bf16x8 kf = *reinterpret_cast<const bf16x8*>(Kw + att_off(kb * 32 + krow, 2 * kk + hi));
       s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[kk], s[kb], 0, 0, 0);
     }
   }
+  // accumulator v of block kb holds key key0 + kb*32 + 16*(v/8) + 8*hi + v%8
   float mx = -INFINITY;
 #pragma unroll
   for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
     for (int v = 0; v < 16; ++v) {
-      const int key = key0 + kb * 32 + 8 * (v >> 2) + 4 * hi + (v & 3);
+      const int key = key0 + kb * 32 + 16 * (v >> 3) + 8 * hi + (v & 7);
       const float sv = key < kv ? s[kb][v] * scale_log2 : -INFINITY;
       s[kb][v] = sv;
       mx = fmaxf(mx, sv);
@@ -370,17 +374,22 @@ decode_attention_kernel(const uint16_t* __restrict__ qk, long ldqk, const uint16
   for (int b = 0; b < 2; ++b)
 #pragma unroll
     for (int v = 0; v < 16; ++v) o[b][v] = 0.f;
+  // O^T[d][q] += V^T[d][keys] P^T[keys][q]; k-step (kb, half) = keys kb*32 + 16*half + [0, 16)
 #pragma unroll
   for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
     for (int half = 0; half < 2; ++half) {
-      bf16x8 pf;
+      floatx8 pv;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) pf[j] = (__bf16)s[kb][8 * half + j];
+      for (int j = 0; j < 8; ++j) pv[j] = s[kb][8 * half + j];
+      const bf16x8 pf = __builtin_convertvector(pv, bf16x8);
 #pragma unroll
-      for (int db = 0; db < 2; ++db)
-        o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[kb][half][db], pf, o[db], 0, 0, 0);
+      for (int db = 0; db < 2; ++db) {
+        const bf16x8 vf = *reinterpret_cast<const bf16x8*>(Vw + att_off(db * 32 + l32, 4 * kb + 2 * half + hi));
+        o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf, o[db], 0, 0, 0);
+      }
     }
+  __syncthreads();  // every wave is done with its tiles: their space becomes Ow
   // O^T[d][q] in lanes: q = l32, d = db*32 + 8*(v/4) + 4*hi + v%4
 #pragma unroll
   for (int db = 0; db < 2; ++db)
