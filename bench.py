@@ -7,10 +7,11 @@ weights N(0, 0.02), contexts N(0,1), noise N(0,1), g_cond = 0.
 
 Prints one JSON line:
   value        DiT GEMM TFLOP/s = executed GEMM FLOPs per solve / wall-per-solve:
-               NFE * [11 * 2*M*(4H^2 + 2HF) + 2*M*3H^2 + 2*N*P*(H^2 + 2HF)],
-               M = sum(c_i + 16) unpadded rows; the last block's O projection and
-               MLP run on the N*P latent rows only, the rows the caller keeps
-               (reference_equivalent_tflops counts 12 full blocks instead)
+               NFE * [11 * 2*M*(4H^2 + 2HF) + 2*M*2H^2 + 2*N*P*(2H^2 + 2HF)],
+               M = sum(c_i + 16) unpadded rows; the last block projects K|V over
+               every row and Q, O and the MLP over the N*P latent rows only, the
+               rows the caller keeps (reference_equivalent_tflops counts 12 full
+               blocks instead)
   roofline     the dominant GEMM (largest total time) timed with dispatch-packet
                HIP events inside the timed region
   cpu_baseline the oracle's float32 DiT on the host cores over a bounded
@@ -333,10 +334,11 @@ def main():
 
     H, F = cfg.hidden, cfg.ffn
     ref_gemm_flops = R.dit_gemm_flops(cfg, M) * 4
-    # GEMM FLOPs the solve executes: the last block runs QKV over every row and
-    # the O projection and MLP over the n*P latent rows only (latent tail)
+    # GEMM FLOPs the solve executes: the last block projects K|V over every row
+    # and Q, O and the MLP over the n*P latent rows only (latent tail)
     NP = n * cfg.patch
-    gemm_flops = 4 * (R.dit_gemm_flops(cfg, M) - M * 2 * (H * H + 2 * H * F) + NP * 2 * (H * H + 2 * H * F))
+    gemm_flops = 4 * (R.dit_gemm_flops(cfg, M) - M * 2 * (2 * H * H + 2 * H * F)
+                      + NP * 2 * (2 * H * H + 2 * H * F))
     tflops = gemm_flops / (ms * 1e-3) / 1e12
     xrt = n * cfg.patch * FRAME_S / (ms * 1e-3)
     per_launch = {"qkv_gemm": 2 * M * H * 3 * H, "o_gemm": 2 * M * H * H,
@@ -355,9 +357,8 @@ def main():
     breakdown = {k: {"ms_per_solve": v[0] / args.steps, "launches_per_solve": v[1] / args.steps}
                  for k, v in classes.items()}
     gemm_ms = sum(role_ms.values()) / args.steps
-    gemm_flops_big = 4 * (cfg.n_blocks * per_launch["qkv_gemm"]
-                          + (cfg.n_blocks - 1) * (per_launch["o_gemm"] + per_launch["fc1_gemm"]
-                                                  + per_launch["fc2_gemm"]))
+    gemm_flops_big = 4 * (cfg.n_blocks - 1) * (per_launch["qkv_gemm"] + per_launch["o_gemm"]
+                                               + per_launch["fc1_gemm"] + per_launch["fc2_gemm"])
     log("per-class ms/solve: " + ", ".join(f"{k}={v['ms_per_solve']:.3f}" for k, v in breakdown.items()))
 
     vl = varlen_bench(mf, hist, noise_d, g_d, out)

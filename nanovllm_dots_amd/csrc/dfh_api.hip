@@ -93,7 +93,7 @@ struct DfhHandle {
   long cap_M = 0, ld_vt = 0;
   DevBuf seq, x, hbuf, qk, attn, ff, vt;
   DevBuf row_req, row_pos, vt_col, cu_rows, cu_vt, hist_len, counts, err, patch_rows, seqs;
-  DevBuf tail_seqs, tail_req;  // last block on the latent rows only: their queries, compact row -> request
+  DevBuf tail_seqs, tail_req, tail_pos;  // last block on the latent rows: queries, row -> request / position
   DevBuf rope_cos, rope_sin;
   DevBuf temb_in, t_hid, t_out, d_hid, d_out, cond, cond_act, mod;
   DevBuf z, zp, fin, vel, tvals;
@@ -224,6 +224,7 @@ int reserve(DfhHandle* h, int n, int T, int S, hipStream_t s) {
   DFH_CHECK(dev_alloc(h->seqs, (long)nn * SS * sizeof(AttnSeq)));
   DFH_CHECK(dev_alloc(h->tail_seqs, (long)nn * sizeof(AttnSeq)));
   DFH_CHECK(dev_alloc(h->tail_req, (long)nn * P * 4));
+  DFH_CHECK(dev_alloc(h->tail_pos, (long)nn * P * 4));
   DFH_CHECK(dev_alloc(h->rope_cos, (size_t)((TT + 31) / 32) * 32 * 32 * 4));  // whole 32-position groups
   DFH_CHECK(dev_alloc(h->rope_sin, (size_t)((TT + 31) / 32) * 32 * 32 * 4));
   const long RS = (long)SS > nn ? SS : nn;  // timestep rows: per step (solve) or per request (forward)
@@ -311,18 +312,27 @@ struct Pass {
   const AttnSeq* tail_seqs = nullptr;  // [n_seq]: the latent queries, output row j
   const int* tail_rows = nullptr;      // [n_tail]: pass row of compact row j
   const int* tail_req = nullptr;       // [n_tail]: request of compact row j
+  const int* tail_pos = nullptr;       // [n_tail]: position of compact row j
   int n_tail = 0;
 };
 
-// The last block on the latent rows only (Pass::latent_tail), after its QKV
-// GEMM over every row. Per row the same operations as the full block; rows
-// that no output depends on are not computed.
-int run_latent_tail(DfhHandle* h, const Pass& p, int l, const uint16_t* ml, long ldm, hipStream_t s) {
+// The last block on the latent rows only (Pass::latent_tail), after its K|V
+// GEMM over every row (q_args: that GEMM's arguments, for the latent rows' Q).
+// Per row the same operations as the full block; rows that no output depends
+// on are not computed.
+int run_latent_tail(DfhHandle* h, const Pass& p, int l, const uint16_t* ml, long ldm, const GemmArgs& q_args,
+                    hipStream_t s) {
   const DfhConfig& c = h->cfg;
   const int H = c.hidden, F = c.ffn, NT = p.n_tail;
   uint16_t* xl = P<uint16_t>(h->hbuf);  // compact residual rows (hbuf's LN output is consumed)
   uint16_t* hl = P<uint16_t>(h->x);     // compact LN output (x is dead once gathered)
   uint16_t* al = P<uint16_t>(h->attn);  // compact attention output
+  // Q of the latent rows: their LayerNorm rows compact in al, q written to their q|k rows
+  DFH_CHECK(gather_rows(P<uint16_t>(h->hbuf), p.tail_rows, nullptr, NT, H, al, s));
+  GemmArgs qa = q_args;
+  qa.A = al; qa.lda = H; qa.B = h->qkv_w[l]; qa.ldb = H; qa.N = H; qa.col0 = 0;
+  qa.M = NT; qa.M_dev = nullptr; qa.row_pos = p.tail_pos; qa.c_rows = p.tail_rows;
+  DFH_CHECK(gemm(h, PC_TAIL, qa, EPI_QKV, s));
   DFH_CHECK(gather_rows(P<uint16_t>(h->x), p.tail_rows, nullptr, NT, H, xl, s));
   prof_arm(h, PC_TAIL);
   DFH_CHECK(attention_worklist(p.tail_seqs, p.n_seq, h->attq.p, s));
@@ -372,9 +382,16 @@ int run_blocks(DfhHandle* h, const Pass& p, hipStream_t s) {
     q.qk_norm = c.qk_norm;
     q.qn_w = h->qn_w[l]; q.qn_b = h->qn_b[l]; q.kn_w = h->kn_w[l]; q.kn_b = h->kn_b[l];
     q.vt = p.vt[l]; q.ld_vt = p.ld_vt; q.vt_col = p.vt_col; q.c_rows = p.c_rows;
+    if ((p.latent_tail || p.kv_only_last) && l == c.n_blocks - 1) {
+      // no query of these rows is used in the last block: K|V over every row
+      // (a prefix pass stops there; a latent tail projects the latent rows' Q)
+      GemmArgs kv = q;
+      kv.B = h->qkv_w[l] + (long)H * H; kv.N = 2 * H; kv.col0 = H;
+      DFH_CHECK(gemm(h, p.kv_only_last ? PC_QKV : PC_TAIL, kv, EPI_QKV, s, tile_for(Mup, 2 * H, H, kRoleQKV)));
+      if (p.kv_only_last) break;
+      return run_latent_tail(h, p, l, ml, ldm, q, s);
+    }
     DFH_CHECK(gemm(h, PC_QKV, q, EPI_QKV, s, tile_for(Mup, 3 * H, H, kRoleQKV)));
-    if (p.kv_only_last && l == c.n_blocks - 1) break;
-    if (p.latent_tail && l == c.n_blocks - 1) return run_latent_tail(h, p, l, ml, ldm, s);
     prof_arm(h, PC_ATTN);
     if (p.decode)
       DFH_CHECK(decode_attention(p.qk[l], p.ldqk, p.vt[l], p.ld_vt, P<uint16_t>(h->attn), H, p.seqs, p.n_seq,
@@ -423,6 +440,7 @@ int dit_blocks(DfhHandle* h, int n, int T, long mod_row0, hipStream_t s, bool la
     p.tail_seqs = P<AttnSeq>(h->tail_seqs);
     p.tail_rows = P<int>(h->patch_rows);
     p.tail_req = P<int>(h->tail_req);
+    p.tail_pos = P<int>(h->tail_pos);
     p.n_tail = n * c.patch;
   }
   return run_blocks(h, p, s);
@@ -435,7 +453,8 @@ int layout(DfhHandle* h, int n, int T, const void* pos_ids, const void* inp, hip
   const DfhConfig& c = h->cfg;
   DFH_CHECK(fm_layout(reinterpret_cast<const float*>(pos_ids), lens, n, T, c.patch, P<int>(h->cu_rows),
                       P<int>(h->cu_vt), P<int>(h->hist_len), P<int>(h->counts), P<int>(h->err),
-                      P<AttnSeq>(h->seqs), P<AttnSeq>(h->tail_seqs), P<int>(h->tail_req), s));
+                      P<AttnSeq>(h->seqs), P<AttnSeq>(h->tail_seqs), P<int>(h->tail_req), P<int>(h->tail_pos),
+                      s));
   DFH_CHECK(fm_gather(reinterpret_cast<const uint16_t*>(inp), src_rows, src_stride, n, T, c.patch, c.hidden,
                       P<int>(h->cu_rows), P<int>(h->cu_vt), P<int>(h->hist_len), P<uint16_t>(h->seq),
                       P<int>(h->row_req), P<int>(h->row_pos), P<int>(h->vt_col),

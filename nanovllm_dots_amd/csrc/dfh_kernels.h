@@ -47,6 +47,7 @@ struct GemmArgs {
   const uint16_t* kn_w; const uint16_t* kn_b;
   uint16_t* vt; long ld_vt; const int* vt_col;   // V^T [hidden, ld_vt]; column of row m = vt_col[m]
   const int* c_rows;                             // optional: q|k output row of row m
+  int col0;                                      // fused q|k|v column of B's first row (0, or hidden: k|v only)
   // Optional K-split of the last, partial round of tiles: each XCD's leftover
   // tiles are cut along K over its idle workgroups; partial sums go to ws and the
   // workgroup that completes a tile adds them and runs the epilogue. ws_elems

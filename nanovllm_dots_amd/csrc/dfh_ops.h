@@ -14,10 +14,11 @@ struct TimeVals {
 
 // Request layout from pos_ids (padded inputs) or from lens (varlen inputs).
 // Optional: tail_seqs [n] (the P latent queries of each request, output rows
-// i*P + j) and tail_req [n*P] (request of compact latent row i*P + j).
+// i*P + j), tail_req [n*P] and tail_pos [n*P] (request and position of compact
+// latent row i*P + j).
 hipError_t fm_layout(const float* pos_ids, const int* lens, int n, int T, int P, int* cu_rows, int* cu_vt,
                      int* hist_len, int* counts, int* err, AttnSeq* seqs, AttnSeq* tail_seqs, int* tail_req,
-                     hipStream_t s);
+                     int* tail_pos, hipStream_t s);
 hipError_t prefix_tables(const uint16_t* rows_in, long stride_in, int m_max, int H, const int* counts,
                          const int* lens, const int* offs, int n, int S, int cap, uint16_t* seq, int* row_req,
                          int* row_pos, int* c_rows, int* vt_col, AttnSeq* seqs, hipStream_t s);

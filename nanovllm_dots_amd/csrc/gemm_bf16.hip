@@ -301,6 +301,7 @@ template <class C, class ACC>
 __device__ __forceinline__ void qkv_epilogue(const GemmArgs& a, ACC (&acc)[C::RN][C::RM], int m0, int n0,
                                              int M, int wm, int wn, int l32, int hi) {
   const int H = a.hidden;
+  n0 += a.col0;               // column within the fused q|k|v output
   const int region = n0 / H;  // 0 q, 1 k, 2 v (BN divides H)
 #pragma unroll
   for (int k = 0; k < C::RM; ++k) {

@@ -94,7 +94,7 @@ __global__ void __launch_bounds__(1024)
 fm_layout_kernel(const float* __restrict__ pos_ids, const int* __restrict__ lens, int n, int T, int P,
                  int* __restrict__ cu_rows, int* __restrict__ cu_vt, int* __restrict__ hist_len,
                  int* __restrict__ counts, int* __restrict__ err, AttnSeq* __restrict__ seqs,
-                 AttnSeq* __restrict__ tail_seqs, int* __restrict__ tail_req) {
+                 AttnSeq* __restrict__ tail_seqs, int* __restrict__ tail_req, int* __restrict__ tail_pos) {
   __shared__ int s_rows[1024], s_vt[1024];
   const int i = threadIdx.x;
   int c = 0;
@@ -138,6 +138,8 @@ fm_layout_kernel(const float* __restrict__ pos_ids, const int* __restrict__ lens
     if (tail_seqs) tail_seqs[i] = AttnSeq{r0, r0, v0, c, Ti, c - 1, Ti, i * P - c};
     if (tail_req)
       for (int j = 0; j < P; ++j) tail_req[i * P + j] = i;
+    if (tail_pos)
+      for (int j = 0; j < P; ++j) tail_pos[i * P + j] = c + j;
   }
   if (i == 0) {
     cu_rows[0] = 0;
@@ -414,10 +416,10 @@ hipError_t ln_modulate(const uint16_t* x, long ldx, uint16_t* out, long ldo, con
 
 hipError_t fm_layout(const float* pos_ids, const int* lens, int n, int T, int P, int* cu_rows, int* cu_vt,
                      int* hist_len, int* counts, int* err, AttnSeq* seqs, AttnSeq* tail_seqs, int* tail_req,
-                     hipStream_t s) {
+                     int* tail_pos, hipStream_t s) {
   if (n <= 0 || n > 1024 || (!pos_ids && !lens)) return hipErrorInvalidValue;
   hipLaunchKernelGGL(fm_layout_kernel, dim3(1), dim3(1024), 0, s, pos_ids, lens, n, T, P, cu_rows, cu_vt,
-                     hist_len, counts, err, seqs, tail_seqs, tail_req);
+                     hist_len, counts, err, seqs, tail_seqs, tail_req, tail_pos);
   return hipGetLastError();
 }
 
