@@ -256,6 +256,9 @@ def test_full_size_nfe4_solve():
                                             # fewer tiles than resident workgroups: every tile is split
                                             (68, 4096, 1024, 3, 4), (68, 1024, 4096, 3, 1), (68, 1024, 1024, 3, 0),
                                             (1024, 1024, 4096, 2, 4), (1024, 4096, 1024, 3, 4), (5, 4096, 256, 3, 4),
+                                            # the O projection and QKV shapes at 36,937 rows; a 9000-row O
+                                            (36937, 1024, 1024, 2, 4), (36937, 1024, 3072, 8, 0),
+                                            (9000, 1024, 1024, 2, 1),
                                             (20000, 1024, 4096, 0, 4), (3000, 2048, 256, 3, 4),
                                             (700, 1024, 256, 3, 0)])
 def test_gemm_ksplit_matches_whole_tiles(M, K, N, tile, epi):
@@ -268,7 +271,7 @@ def test_gemm_ksplit_matches_whole_tiles(M, K, N, tile, epi):
     B = (0.02 * torch.randn(N, K, generator=g)).bfloat16().cuda()
     bias = (0.1 * torch.randn(N, generator=g)).bfloat16().cuda()
     dt = torch.float32 if epi == 4 else torch.bfloat16
-    ws = torch.zeros((1 << 26) + (1 << 16), dtype=torch.uint8, device="cuda")  # zero-filled before first use
+    ws = torch.zeros((1 << 27) + (1 << 16), dtype=torch.uint8, device="cuda")  # zero-filled before first use
     outs = []
     for use_ws in (False, True):
         C = torch.zeros((M, N), device="cuda", dtype=dt)
