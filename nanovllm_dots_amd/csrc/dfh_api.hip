@@ -92,6 +92,7 @@ struct DfhHandle {
   int cap_n = 0, cap_T = 0, cap_S = 0;
   long cap_M = 0, ld_vt = 0;
   DevBuf seq, x, hbuf, qk, attn, ff, vt;
+  DevBuf x0;  // solve: input_layer of every packed row, once per solve (latent rows per step)
   DevBuf row_req, row_pos, vt_col, cu_rows, cu_vt, hist_len, counts, err, patch_rows, seqs;
   DevBuf tail_seqs, tail_req, tail_pos;  // last block on the latent rows: queries, row -> request / position
   DevBuf rope_cos, rope_sin;
@@ -182,6 +183,7 @@ int reserve_rows(DfhHandle* h, long M, hipStream_t s) {
   const long H = c.hidden, F = c.ffn, ld = c.latent_dim;
   DFH_CHECK(dev_alloc(h->seq, M * H * 2));
   DFH_CHECK(dev_alloc(h->x, M * H * 2));
+  DFH_CHECK(dev_alloc(h->x0, M * H * 2));
   DFH_CHECK(dev_alloc(h->hbuf, M * H * 2));
   DFH_CHECK(dev_alloc(h->qk, M * 2 * H * 2));
   DFH_CHECK(dev_alloc(h->attn, M * H * 2));
@@ -303,6 +305,9 @@ struct Pass {
   bool decode = false;         // split-KV decode attention (<= 32 queries / sequence)
   float* part = nullptr;       // decode partials
   bool kv_only_last = false;   // prefix pass: the last block only has to leave its K/V
+  // input_layer rows computed before the pass (solve: the history rows once per
+  // solve, the latent rows per step): block 0 reads them and writes h->x
+  const uint16_t* x0 = nullptr;
   // Only the latent rows' block output is consumed (FM solve: the caller keeps
   // v[:, -P:], batched_fm.py:122-124). The last block then runs LN + QKV on
   // every row (the latent queries attend over every row's K/V) and attention,
@@ -321,11 +326,11 @@ struct Pass {
 // Per row the same operations as the full block; rows that no output depends
 // on are not computed.
 int run_latent_tail(DfhHandle* h, const Pass& p, int l, const uint16_t* ml, long ldm, const GemmArgs& q_args,
-                    hipStream_t s) {
+                    const uint16_t* xin, hipStream_t s) {
   const DfhConfig& c = h->cfg;
   const int H = c.hidden, F = c.ffn, NT = p.n_tail;
   uint16_t* xl = P<uint16_t>(h->hbuf);  // compact residual rows (hbuf's LN output is consumed)
-  uint16_t* hl = P<uint16_t>(h->x);     // compact LN output (x is dead once gathered)
+  uint16_t* hl = P<uint16_t>(h->x);     // compact LN output (x is dead once gathered; x0 is not written)
   uint16_t* al = P<uint16_t>(h->attn);  // compact attention output
   // Q of the latent rows: their LayerNorm rows compact in al, q written to their q|k rows
   DFH_CHECK(gather_rows(P<uint16_t>(h->hbuf), p.tail_rows, nullptr, NT, H, al, s));
@@ -333,7 +338,7 @@ int run_latent_tail(DfhHandle* h, const Pass& p, int l, const uint16_t* ml, long
   qa.A = al; qa.lda = H; qa.B = h->qkv_w[l]; qa.ldb = H; qa.N = H; qa.col0 = 0;
   qa.M = NT; qa.M_dev = nullptr; qa.row_pos = p.tail_pos; qa.c_rows = p.tail_rows;
   DFH_CHECK(gemm(h, PC_TAIL, qa, EPI_QKV, s));
-  DFH_CHECK(gather_rows(P<uint16_t>(h->x), p.tail_rows, nullptr, NT, H, xl, s));
+  DFH_CHECK(gather_rows(xin, p.tail_rows, nullptr, NT, H, xl, s));  // the block's input rows
   prof_arm(h, PC_TAIL);
   DFH_CHECK(attention_worklist(p.tail_seqs, p.n_seq, h->attq.p, s));
   prof_arm(h, PC_TAIL);
@@ -365,13 +370,16 @@ int run_blocks(DfhHandle* h, const Pass& p, hipStream_t s) {
   // attention work list of this pass (its sequences are fixed for all blocks)
   if (!p.decode) DFH_CHECK(attention_worklist(p.seqs, p.n_seq, h->attq.p, s));
   // input_layer
-  DFH_CHECK(gemm(h, PC_OTHER, linear_args(P<uint16_t>(h->seq), H, h->in_w, h->in_b,
-                                          P<uint16_t>(h->x), H, Mup, Md, H, H), EPI_BIAS, s,
-                 tile_for(Mup, H, H, kRoleNarrow)));
+  if (!p.x0)
+    DFH_CHECK(gemm(h, PC_OTHER, linear_args(P<uint16_t>(h->seq), H, h->in_w, h->in_b,
+                                            P<uint16_t>(h->x), H, Mup, Md, H, H), EPI_BIAS, s,
+                   tile_for(Mup, H, H, kRoleNarrow)));
   for (int l = 0; l < c.n_blocks; ++l) {
     const uint16_t* ml = mod + (long)l * 6 * H;  // shift_a, scale_a, gate_a, shift_f, scale_f, gate_f
+    // block 0 of a pass with hoisted input rows reads them; its first gate-residual writes h->x
+    const uint16_t* xin = (l == 0 && p.x0) ? p.x0 : P<uint16_t>(h->x);
     prof_arm(h, PC_LN);
-    DFH_CHECK(ln_modulate(P<uint16_t>(h->x), H, P<uint16_t>(h->hbuf), H, ml + 0 * H, ml + 1 * H, ldm,
+    DFH_CHECK(ln_modulate(xin, H, P<uint16_t>(h->hbuf), H, ml + 0 * H, ml + 1 * H, ldm,
                           row_req, nullptr, Mup, Md, H, c.ln_eps, s));
     GemmArgs q = linear_args(P<uint16_t>(h->hbuf), H, h->qkv_w[l], h->qkv_b[l], p.qk[l], p.ldqk, Mup, Md,
                              3 * H, H);
@@ -389,7 +397,7 @@ int run_blocks(DfhHandle* h, const Pass& p, hipStream_t s) {
       kv.B = h->qkv_w[l] + (long)H * H; kv.N = 2 * H; kv.col0 = H;
       DFH_CHECK(gemm(h, p.kv_only_last ? PC_QKV : PC_TAIL, kv, EPI_QKV, s, tile_for(Mup, 2 * H, H, kRoleQKV)));
       if (p.kv_only_last) break;
-      return run_latent_tail(h, p, l, ml, ldm, q, s);
+      return run_latent_tail(h, p, l, ml, ldm, q, xin, s);
     }
     DFH_CHECK(gemm(h, PC_QKV, q, EPI_QKV, s, tile_for(Mup, 3 * H, H, kRoleQKV)));
     prof_arm(h, PC_ATTN);
@@ -402,6 +410,7 @@ int run_blocks(DfhHandle* h, const Pass& p, hipStream_t s) {
     GemmArgs o = linear_args(P<uint16_t>(h->attn), H, h->o_w[l], h->o_b[l], P<uint16_t>(h->x), H,
                              Mup, Md, H, H);
     o.gate = ml + 2 * H; o.ld_gate = ldm; o.row_req = row_req;
+    if (xin != P<uint16_t>(h->x)) { o.res = xin; o.ld_res = H; }
     DFH_CHECK(gemm(h, PC_O, o, EPI_GATE_RES, s, tile_for(Mup, H, H, kRoleNarrow)));
     prof_arm(h, PC_LN);
     DFH_CHECK(ln_modulate(P<uint16_t>(h->x), H, P<uint16_t>(h->hbuf), H, ml + 3 * H, ml + 4 * H, ldm,
@@ -419,7 +428,8 @@ int run_blocks(DfhHandle* h, const Pass& p, hipStream_t s) {
 
 // The FM pass over the packed requests of layout(): rows m of h->seq, request
 // row_req[m], q|k into the workspace, V^T in h->vt.
-int dit_blocks(DfhHandle* h, int n, int T, long mod_row0, hipStream_t s, bool latent_tail = false) {
+int dit_blocks(DfhHandle* h, int n, int T, long mod_row0, hipStream_t s, bool latent_tail = false,
+               const uint16_t* x0 = nullptr) {
   const DfhConfig& c = h->cfg;
   Pass p;
   p.Mup = n * T;
@@ -435,6 +445,7 @@ int dit_blocks(DfhHandle* h, int n, int T, long mod_row0, hipStream_t s, bool la
   p.seqs = P<AttnSeq>(h->seqs);
   p.n_seq = n;
   p.max_q = T;
+  p.x0 = x0;
   if (latent_tail) {
     p.latent_tail = true;
     p.tail_seqs = P<AttnSeq>(h->tail_seqs);
@@ -478,13 +489,20 @@ int solve_steps(DfhHandle* h, int n, int T, int S, const void* g_cond, const voi
     return 1;
   DFH_CHECK(hipMemcpyAsync(h->z.p, noise, (size_t)n * Pp * ld * 2, hipMemcpyDeviceToDevice, s));
   const int NP = n * Pp;
+  // input_layer of every packed row once: a history row's does not depend on the
+  // step (no t or z); the latent rows' are replaced every step
+  DFH_CHECK(gemm(h, PC_OTHER, linear_args(P<uint16_t>(h->seq), H, h->in_w, h->in_b, P<uint16_t>(h->x0), H,
+                                          n * T, P<int>(h->counts), H, H), EPI_BIAS, s,
+                 tile_for(n * T, H, H, kRoleNarrow)));
   for (int st = 0; st < S; ++st) {
-    // zp = coordinate_proj(z) -> latent rows of the packed sequence
+    // zp = coordinate_proj(z); its input_layer rows -> the latent rows of x0
     DFH_CHECK(gemm(h, PC_OTHER, linear_args(P<uint16_t>(h->z), ld, h->coord_w, h->coord_b,
                                             P<uint16_t>(h->zp), H, NP, nullptr, H, ld), EPI_BIAS, s));
-    DFH_CHECK(scatter_rows(P<uint16_t>(h->zp), P<int>(h->patch_rows), NP, H, P<uint16_t>(h->seq), s));
+    DFH_CHECK(gemm(h, PC_OTHER, linear_args(P<uint16_t>(h->zp), H, h->in_w, h->in_b, P<uint16_t>(h->fin), H,
+                                            NP, nullptr, H, H), EPI_BIAS, s));
+    DFH_CHECK(scatter_rows(P<uint16_t>(h->fin), P<int>(h->patch_rows), NP, H, P<uint16_t>(h->x0), s));
     const bool tail = h->latent_tail;
-    if (dit_blocks(h, n, T, (long)st * n, s, tail)) return 1;
+    if (dit_blocks(h, n, T, (long)st * n, s, tail, P<uint16_t>(h->x0))) return 1;
     // FinalLayer on the latent rows only (compact in h->hbuf after a latent tail)
     const uint16_t* mf = P<uint16_t>(h->mod) + (long)st * n * h->ld_mod + (long)c.n_blocks * 6 * H;
     prof_arm(h, tail ? PC_TAIL : PC_LN);
@@ -537,7 +555,8 @@ int dfh_destroy(DfhHandle* h) {
                     &h->vt, &h->row_req, &h->row_pos, &h->vt_col, &h->cu_rows, &h->cu_vt,
                     &h->hist_len, &h->counts, &h->err, &h->patch_rows, &h->seqs, &h->rope_cos, &h->rope_sin,
                     &h->temb_in, &h->t_hid, &h->t_out, &h->d_hid, &h->d_out, &h->cond,
-                    &h->cond_act, &h->mod, &h->z, &h->zp, &h->fin, &h->vel, &h->tvals, &h->splitws, &h->attq};
+                    &h->cond_act, &h->mod, &h->z, &h->zp, &h->fin, &h->vel, &h->tvals, &h->splitws, &h->attq,
+                    &h->x0, &h->tail_seqs, &h->tail_req, &h->tail_pos};
   for (DevBuf* b : bufs)
     if (b->p) (void)hipFree(b->p);
   for (hipEvent_t ev : h->ev_pool) (void)hipEventDestroy(ev);

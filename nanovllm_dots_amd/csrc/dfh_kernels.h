@@ -36,8 +36,9 @@ struct GemmArgs {
   const uint16_t* bias;              // [N] or null
   int M; const int* M_dev;           // rows; M_dev (device int) overrides M when non-null
   int N, K;
-  // EPI_GATE_RES
+  // EPI_GATE_RES (res: residual source rows, ld_res; null: C itself, updated in place)
   const uint16_t* gate; long ld_gate; const int* row_req;
+  const uint16_t* res; long ld_res;
   // EPI_QKV
   int hidden, head_dim;
   const float* rope_cos; const float* rope_sin;  // [max_pos, head_dim/2] or null (no rotary)

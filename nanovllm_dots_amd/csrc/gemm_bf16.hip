@@ -175,7 +175,7 @@ __device__ __forceinline__ void res_block_load(const GemmArgs& a, const ResRows<
   for (int j = 0; j < S::JB; ++j) {
     const int m = m0 + wm * C::WTM + k * 32 + j * S::RPI + lane / S::CPR;
     const int mm = m < M ? m : M - 1;
-    x[j] = *reinterpret_cast<const uint4*>(a.C + (long)mm * a.ldc + n);
+    x[j] = *reinterpret_cast<const uint4*>(a.res ? a.res + (long)mm * a.ld_res + n : a.C + (long)mm * a.ldc + n);
     g[j] = *reinterpret_cast<const uint4*>(a.gate + (long)rr.rq[k * S::JB + j] * a.ld_gate + n);
   }
 }
@@ -442,7 +442,7 @@ __device__ __forceinline__ void run_epilogue(const GemmArgs& a, ACC (&acc)[C::RN
         const int r = wm * C::WTM + k * 32 + l32;  // row within the tile
         const int mm = m0 + r < M ? m0 + r : M - 1;
         const uint32_t rowoff = (uint32_t)r * (uint32_t)a.ldc;
-        const uint16_t* xrow = a.C + (long)mm * a.ldc;
+        const uint16_t* xrow = a.res ? a.res + (long)mm * a.ld_res : a.C + (long)mm * a.ldc;
         const uint16_t* grow = nullptr;
         if constexpr (EPI == EPI_GATE_RES) grow = a.gate + (long)a.row_req[mm] * a.ld_gate;
         float sxm = 0.f;
