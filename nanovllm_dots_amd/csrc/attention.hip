@@ -207,7 +207,7 @@ seq_attention_kernel(const uint16_t* __restrict__ qk, long ldqk, const uint16_t*
     for (int v = 2; v < 16; ++v) mx = fmaxf(mx, s[0][v]);
 #pragma unroll
     for (int v = 0; v < 16; ++v) mx = fmaxf(mx, s[1][v]);
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    mx = fmaxf(mx, swap_halves(mx));
     if (__any(mx > m_run + thr)) {
       const float m_new = fmaxf(m_run, mx);
       const float alpha = __builtin_amdgcn_exp2f((m_run - m_new) * scale_log2);
@@ -260,7 +260,7 @@ seq_attention_kernel(const uint16_t* __restrict__ qk, long ldqk, const uint16_t*
     compute(K1, V1, (t + 1) * BKV);
   }
 
-  const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
+  const float l_tot = l_run + swap_halves(l_run);
   if (q < sq.q_end) {
     const float inv = 1.0f / l_tot;
     uint16_t* op = out + (long)(sq.out_row0 + q) * ldo + h * HD;
@@ -357,7 +357,7 @@ decode_attention_kernel(const uint16_t* __restrict__ qk, long ldqk, const uint16
       s[kb][v] = sv;
       mx = fmaxf(mx, sv);
     }
-  mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+  mx = fmaxf(mx, swap_halves(mx));
   const float m_safe = mx == -INFINITY ? 0.f : mx;  // a wave entirely past kv_len
   float psum = 0.f;
 #pragma unroll
@@ -368,7 +368,7 @@ decode_attention_kernel(const uint16_t* __restrict__ qk, long ldqk, const uint16
       s[kb][v] = p;
       psum += p;
     }
-  psum += __shfl_xor(psum, 32, 64);
+  psum += swap_halves(psum);
   floatx16 o[2];
 #pragma unroll
   for (int b = 0; b < 2; ++b)

@@ -82,6 +82,14 @@ __device__ __forceinline__ float gelu_tanh_f(float x) {
 
 __device__ __forceinline__ float silu_f(float x) { return x / (1.0f + expf(-x)); }
 
+// value of lane l ^ 32 (the other half of the wave): one v_permlane32_swap,
+// which exchanges lanes 32..63 of its first operand with lanes 0..31 of its
+// second, instead of a ds_bpermute round trip through the LDS crossbar
+__device__ __forceinline__ float swap_halves(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float((threadIdx.x & 32) ? r[0] : r[1]);
+}
+
 // wave-wide reductions (64 lanes)
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
