@@ -54,6 +54,34 @@ __device__ __forceinline__ int att_off(int r, int c) { return r * 64 + ((c ^ ((r
 // row index with bits 2 and 3 swapped
 __device__ __forceinline__ int key_perm(int x) { return (x & ~12) | ((x & 4) << 1) | ((x & 8) >> 1); }
 
+// RoPE of a query row held as MFMA B fragments: lane half hi holds dims
+// 16*kk + 8*hi + [0, 8) in qf[kk]; the rotation pairs (d, d + 32) are
+// (qf[kk], qf[kk + 2]). Factors from the rope_table layout (positions grouped
+// by 32: for d = 8g + 4h + t, float ((p/32*4 + g)*64 + p%32*2 + h)*4 + t), so
+// one kk needs 8 consecutive floats per table. Same float32 operations as the
+// QKV epilogue's RoPE, each result rounded once to bf16.
+__device__ __forceinline__ void rope_q(bf16x8 (&qf)[4], int pos, int hi, const float* __restrict__ rope_cos,
+                                       const float* __restrict__ rope_sin) {
+#pragma unroll
+  for (int kk = 0; kk < 2; ++kk) {
+    const long o = ((long)((pos >> 5) * 4 + 2 * kk + hi) * 64 + (pos & 31) * 2) * 4;
+    const float4 c0 = *reinterpret_cast<const float4*>(rope_cos + o);
+    const float4 c1 = *reinterpret_cast<const float4*>(rope_cos + o + 4);
+    const float4 s0 = *reinterpret_cast<const float4*>(rope_sin + o);
+    const float4 s1 = *reinterpret_cast<const float4*>(rope_sin + o + 4);
+    const float c[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+    const float sn[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float x0 = (float)qf[kk][j], x1 = (float)qf[kk + 2][j];
+      const float r0 = add_rn(mul_rn(x0, c[j]), mul_rn(-x1, sn[j]));
+      const float r1 = add_rn(mul_rn(x1, c[j]), mul_rn(x0, sn[j]));
+      qf[kk][j] = (__bf16)r0;
+      qf[kk + 2][j] = (__bf16)r1;
+    }
+  }
+}
+
 // One workgroup builds the work list: sequences in order of tile count, most
 // first, each sequence's tiles consecutive and longest (highest index) first.
 // The dispatcher then hands out the longest tiles early, the shortest last, and
@@ -113,7 +141,8 @@ __global__ void __launch_bounds__(1024) attention_worklist_kernel(const AttnSeq*
 __global__ void __launch_bounds__(256, 3)
 seq_attention_kernel(const uint16_t* __restrict__ qk, long ldqk, const uint16_t* __restrict__ vt,
                      long ld_vt, uint16_t* __restrict__ out, long ldo, int heads,
-                     const char* __restrict__ list, float scale_log2) {
+                     const char* __restrict__ list, float scale_log2, const float* __restrict__ rope_cos,
+                     const float* __restrict__ rope_sin) {
   __shared__ __attribute__((aligned(16))) uint16_t K0[BKV * HD];
   __shared__ __attribute__((aligned(16))) uint16_t K1[BKV * HD];
   __shared__ __attribute__((aligned(16))) uint16_t V0[HD * BKV];
@@ -152,6 +181,7 @@ seq_attention_kernel(const uint16_t* __restrict__ qk, long ldqk, const uint16_t*
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) qf[kk] = *reinterpret_cast<const bf16x8*>(qp + 16 * kk);
   }
+  if (rope_cos) rope_q(qf, qc, hi, rope_cos, rope_sin);  // uniform
 
   // DMA: wave w, load j covers tile rows [(4j + w) * 8, +8); lane -> row + lane/8, slot lane%8
   const int dma_r0 = wave * 8 + (lane >> 3);
@@ -294,7 +324,8 @@ constexpr int PART = 32 * 66;  // per chunk: m[32], l[32], O[32][64]
 __global__ void __launch_bounds__(256)
 decode_attention_kernel(const uint16_t* __restrict__ qk, long ldqk, const uint16_t* __restrict__ vt,
                         long ld_vt, const AttnSeq* __restrict__ seqs, int heads, float scale_log2,
-                        float* __restrict__ part, int n_chunks) {
+                        float* __restrict__ part, int n_chunks, const float* __restrict__ rope_cos,
+                        const float* __restrict__ rope_sin) {
   // per wave: K tile [64 keys][64] then V^T tile [64 d][64 keys], 16 KB; after the
   // scores and P.V the same space holds the waves' O^T for the merge
   __shared__ __attribute__((aligned(16))) uint16_t tiles[4 * 2 * BKV * HD];
@@ -333,6 +364,7 @@ decode_attention_kernel(const uint16_t* __restrict__ qk, long ldqk, const uint16
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) qf[kk] = *reinterpret_cast<const bf16x8*>(qp + 16 * kk);
   }
+  if (rope_cos) rope_q(qf, sq.q_begin + qi, hi, rope_cos, rope_sin);  // uniform
   wait_vm_lgkm0<0>();  // this wave's tiles are in LDS (only this wave reads them)
   const int krow = key_perm(l32);
   floatx16 s[2];
@@ -499,24 +531,25 @@ hipError_t attention_worklist(const AttnSeq* seqs, int n_seq, void* list, hipStr
 }
 
 hipError_t seq_attention(const uint16_t* qk, long ldqk, const uint16_t* vt, long ld_vt, uint16_t* out,
-                         long ldo, int heads, const void* list, long max_items, hipStream_t s) {
+                         long ldo, int heads, const void* list, long max_items, const float* rope_cos,
+                         const float* rope_sin, hipStream_t s) {
   if (max_items <= 0) return hipSuccess;
   const float scale_log2 = 0.125f * 1.4426950408889634f;  // head_dim^-0.5 * log2(e)
   const long grid = max_items * heads;
   if (grid > 0x7fffffffL) return hipErrorInvalidValue;
   dfh_launch(seq_attention_kernel, dim3((unsigned)grid), dim3(256), 0, s, qk, ldqk, vt, ld_vt, out, ldo, heads,
-             reinterpret_cast<const char*>(list), scale_log2);
+             reinterpret_cast<const char*>(list), scale_log2, rope_cos, rope_sin);
   return hipGetLastError();
 }
 
 hipError_t decode_attention(const uint16_t* qk, long ldqk, const uint16_t* vt, long ld_vt, uint16_t* out,
                             long ldo, const AttnSeq* seqs, int n_seq, int heads, int max_kv,
-                            float* part, hipStream_t s) {
+                            float* part, const float* rope_cos, const float* rope_sin, hipStream_t s) {
   if (n_seq <= 0 || max_kv <= 0) return hipSuccess;
   const float scale_log2 = 0.125f * 1.4426950408889634f;
   const int n_chunks = (max_kv + DCH - 1) / DCH;
   dfh_launch(decode_attention_kernel, dim3(n_chunks, heads, n_seq), dim3(256), 0, s, qk, ldqk, vt, ld_vt,
-             seqs, heads, scale_log2, part, n_chunks);
+             seqs, heads, scale_log2, part, n_chunks, rope_cos, rope_sin);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(decode_combine_kernel, dim3(heads, n_seq, 32 / DQG), dim3(256), 0, s, part, seqs, heads,

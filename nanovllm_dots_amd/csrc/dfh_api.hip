@@ -343,7 +343,9 @@ int run_latent_tail(DfhHandle* h, const Pass& p, int l, const uint16_t* ml, long
   DFH_CHECK(attention_worklist(p.tail_seqs, p.n_seq, h->attq.p, s));
   prof_arm(h, PC_TAIL);
   DFH_CHECK(seq_attention(p.qk[l], p.ldqk, p.vt[l], p.ld_vt, al, H, c.heads, h->attq.p,
-                          (long)p.n_seq * ((c.patch + 127) / 128), s));
+                          (long)p.n_seq * ((c.patch + 127) / 128),
+                          q_args.rope_q_in_attn ? q_args.rope_cos : nullptr,
+                          q_args.rope_q_in_attn ? q_args.rope_sin : nullptr, s));
   GemmArgs o = linear_args(al, H, h->o_w[l], h->o_b[l], xl, H, NT, nullptr, H, H);
   o.gate = ml + 2 * H; o.ld_gate = ldm; o.row_req = p.tail_req;
   DFH_CHECK(gemm(h, PC_TAIL, o, EPI_GATE_RES, s));
@@ -387,6 +389,11 @@ int run_blocks(DfhHandle* h, const Pass& p, hipStream_t s) {
     q.rope_cos = c.rotary ? P<float>(h->rope_cos) : nullptr;
     q.rope_sin = c.rotary ? P<float>(h->rope_sin) : nullptr;
     q.row_pos = p.row_pos;
+    // without qk-norm the stored q is the bf16 linear output the epilogue would
+    // rotate, so the attention kernel rotates it (same float32 operations)
+    q.rope_q_in_attn = c.rotary && c.qk_norm == 0;
+    const float* aq_cos = q.rope_q_in_attn ? q.rope_cos : nullptr;
+    const float* aq_sin = q.rope_q_in_attn ? q.rope_sin : nullptr;
     q.qk_norm = c.qk_norm;
     q.qn_w = h->qn_w[l]; q.qn_b = h->qn_b[l]; q.kn_w = h->kn_w[l]; q.kn_b = h->kn_b[l];
     q.vt = p.vt[l]; q.ld_vt = p.ld_vt; q.vt_col = p.vt_col; q.c_rows = p.c_rows;
@@ -403,10 +410,10 @@ int run_blocks(DfhHandle* h, const Pass& p, hipStream_t s) {
     prof_arm(h, PC_ATTN);
     if (p.decode)
       DFH_CHECK(decode_attention(p.qk[l], p.ldqk, p.vt[l], p.ld_vt, P<uint16_t>(h->attn), H, p.seqs, p.n_seq,
-                                 c.heads, p.max_kv, p.part, s));
+                                 c.heads, p.max_kv, p.part, aq_cos, aq_sin, s));
     else
       DFH_CHECK(seq_attention(p.qk[l], p.ldqk, p.vt[l], p.ld_vt, P<uint16_t>(h->attn), H, c.heads, h->attq.p,
-                              (long)p.n_seq * ((p.max_q + 127) / 128), s));
+                              (long)p.n_seq * ((p.max_q + 127) / 128), aq_cos, aq_sin, s));
     GemmArgs o = linear_args(P<uint16_t>(h->attn), H, h->o_w[l], h->o_b[l], P<uint16_t>(h->x), H,
                              Mup, Md, H, H);
     o.gate = ml + 2 * H; o.ld_gate = ldm; o.row_req = row_req;

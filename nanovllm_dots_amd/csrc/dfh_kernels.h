@@ -41,7 +41,8 @@ struct GemmArgs {
   const uint16_t* res; long ld_res;
   // EPI_QKV
   int hidden, head_dim;
-  const float* rope_cos; const float* rope_sin;  // [max_pos, head_dim/2] or null (no rotary)
+  const float* rope_cos; const float* rope_sin;  // rope_table layout (grouped by 32 positions) or null
+  int rope_q_in_attn;                            // q leaves without RoPE: the attention kernel rotates it
   const int* row_pos;                            // [M] position of each row within its request
   int qk_norm;                                   // 0 none, 1 LayerNorm(affine), 2 RMSNorm
   const uint16_t* qn_w; const uint16_t* qn_b;    // [head_dim]
@@ -110,8 +111,11 @@ hipError_t attention_worklist(const AttnSeq* seqs, int n_seq, void* list, hipStr
 // 128 queries of one (sequence, head): workgroup v takes item v / heads of
 // `list` (attention_worklist of the same sequences), head v % heads.
 // max_items bounds the item count of the list (e.g. n_seq * ceil(max_q / 128)).
+// rope_cos / rope_sin (rope_table layout, or null): the q rows hold no RoPE yet and
+// query position q of a sequence is rotated here, as the QKV epilogue would.
 hipError_t seq_attention(const uint16_t* qk, long ldqk, const uint16_t* vt, long ld_vt, uint16_t* out,
-                         long ldo, int heads, const void* list, long max_items, hipStream_t s);
+                         long ldo, int heads, const void* list, long max_items, const float* rope_cos,
+                         const float* rope_sin, hipStream_t s);
 
 // Split-KV decode attention: every query of a sequence sees all kv_len keys
 // (q_begin..q_end are at most 32 queries). Keys are read straight from HBM in
@@ -119,7 +123,7 @@ hipError_t seq_attention(const uint16_t* qk, long ldqk, const uint16_t* vt, long
 // part holds n_seq * heads * ceil(max_kv / kv_chunk) * 32 * 66 floats.
 hipError_t decode_attention(const uint16_t* qk, long ldqk, const uint16_t* vt, long ld_vt, uint16_t* out,
                             long ldo, const AttnSeq* seqs, int n_seq, int heads, int max_kv,
-                            float* part, hipStream_t s);
+                            float* part, const float* rope_cos, const float* rope_sin, hipStream_t s);
 
 // Paged attention of appended tokens over a paged (or contiguous) KV cache
 // (flash_attn_varlen_func / flash_attn_with_kvcache semantics, bottom-right

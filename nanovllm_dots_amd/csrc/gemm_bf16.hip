@@ -362,7 +362,7 @@ __device__ __forceinline__ void qkv_epilogue(const GemmArgs& a, ACC (&acc)[C::RN
           x1[v] = (x1[v] - mean) * rstd * w1 + c1;
         }
       }
-      if (a.rope_cos) {
+      if (a.rope_cos && !(region == 0 && a.rope_q_in_attn)) {
         // tables grouped by 32 positions (rope_table): this lane's d = 8g + 4hi + t
         const long to = ((long)(pos >> 5) * 256 + (pos & 31) * 2 + hi) * 4;
         const float* cs = a.rope_cos + to;
