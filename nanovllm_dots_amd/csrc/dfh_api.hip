@@ -390,8 +390,9 @@ int run_blocks(DfhHandle* h, const Pass& p, hipStream_t s) {
     q.rope_sin = c.rotary ? P<float>(h->rope_sin) : nullptr;
     q.row_pos = p.row_pos;
     // without qk-norm the stored q is the bf16 linear output the epilogue would
-    // rotate, so the attention kernel rotates it (same float32 operations)
-    q.rope_q_in_attn = c.rotary && c.qk_norm == 0;
+    // rotate, so the attention kernel rotates it (same float32 operations) once
+    // per (query tile, head); split-KV decode would redo it in every key chunk
+    q.rope_q_in_attn = c.rotary && c.qk_norm == 0 && !p.decode;
     const float* aq_cos = q.rope_q_in_attn ? q.rope_cos : nullptr;
     const float* aq_sin = q.rope_q_in_attn ? q.rope_sin : nullptr;
     q.qk_norm = c.qk_norm;
