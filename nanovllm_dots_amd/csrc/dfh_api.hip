@@ -285,7 +285,8 @@ int build_modulation(DfhHandle* h, int S, int N, bool per_request_t, const float
 }
 
 // One pass of the DiT blocks over packed rows. Input rows are in h->seq
-// (before input_layer); the block output lands in h->x. Row m uses modulation
+// (before input_layer) or, with Pass::x0, already through it; the block output
+// lands in h->x (h->hbuf for the latent rows of a latent tail). Row m uses modulation
 // row mod_row0 + row_req[m], RoPE position row_pos[m], writes its q|k row to
 // qk[l] row c_rows[m] (or m) and its V^T column vt_col[m] in vt[l].
 struct Pass {
@@ -309,10 +310,11 @@ struct Pass {
   // solve, the latent rows per step): block 0 reads them and writes h->x
   const uint16_t* x0 = nullptr;
   // Only the latent rows' block output is consumed (FM solve: the caller keeps
-  // v[:, -P:], batched_fm.py:122-124). The last block then runs LN + QKV on
-  // every row (the latent queries attend over every row's K/V) and attention,
-  // O projection, LN and MLP on the n_tail latent rows alone, compacted in
-  // request order into h->hbuf (rows tail_rows[j] of the pass -> row j).
+  // v[:, -P:], batched_fm.py:122-124). The last block then runs LN and the K|V
+  // projection on every row (the latent queries attend over every row's K/V)
+  // and the Q projection, attention, O projection, LN and MLP on the n_tail
+  // latent rows alone, compacted in request order into h->hbuf (rows
+  // tail_rows[j] of the pass -> row j).
   bool latent_tail = false;
   const AttnSeq* tail_seqs = nullptr;  // [n_seq]: the latent queries, output row j
   const int* tail_rows = nullptr;      // [n_tail]: pass row of compact row j
