@@ -261,6 +261,8 @@ def main():
     ap.add_argument("--no-w8a8", action="store_true")
     ap.add_argument("--no-kvcache", action="store_true")
     ap.add_argument("--no-paged", action="store_true")
+    ap.add_argument("--w8a8-only", action="store_true",
+                    help="run only the W8A8 linears leg (M = 16384, four (K, N) shapes) and print its record")
     ap.add_argument("--kvcache-only", action="store_true",
                     help="run only the KV-cached solve leg (4 streams x 10,111 cached rows) and print its record")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
@@ -278,6 +280,9 @@ def main():
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.w8a8_only:
+        print(json.dumps({"w8a8_m16384": w8a8_bench()}), flush=True)
+        return
     if args.calib_copy_mib:
         src = torch.empty(args.calib_copy_mib << 20, dtype=torch.uint8, device=dev)
         dst = torch.empty_like(src)

@@ -146,6 +146,7 @@ def mfma(path: str, simds: int = 1024, xcds: int = 8):
             "cycles": gui,
             "mfma_util": c.get("SQ_VALU_MFMA_BUSY_CYCLES", 0.0) / (gui * simds),
             "mfma_flop": c.get("SQ_INSTS_VALU_MFMA_MOPS_BF16", 0.0) * 512,
+            "mfma_iop": c.get("SQ_INSTS_VALU_MFMA_MOPS_I8", 0.0) * 512,
             "mfma_insts": c.get("SQ_INSTS_MFMA", 0.0),
             "valu_insts": c.get("SQ_INSTS_VALU", 0.0),
             "trans_insts": c.get("SQ_INSTS_VALU_TRANS_F32", 0.0),
@@ -160,6 +161,11 @@ def mfma(path: str, simds: int = 1024, xcds: int = 8):
 
 
 def mfma_table(by, roles_wanted=("qkv_gemm", "o_gemm", "fc1_gemm", "fc2_gemm", "attention", "ln_modulate")) -> str:
+    """Per-role medians; roles_wanted=None lists every role (kernel) that ran."""
+    if roles_wanted is None:
+        roles_wanted = sorted(by)
+    if any(r["mfma_iop"] for rows in by.values() for r in rows):
+        return _mfma_table_i8(by, roles_wanted)
     lines = ["| role | dispatches | cycles (per XCD) | clock GHz | MFMA busy | bf16 MFMA GFLOP | MFMA insts (M) | "
              "VALU insts (M) | of which transc. (M) | VALU busy | VGPR / AGPR |",
              "|---|---:|---:|---:|---:|---:|---:|---:|---:|---:|---|"]
@@ -172,6 +178,20 @@ def mfma_table(by, roles_wanted=("qkv_gemm", "o_gemm", "fc1_gemm", "fc2_gemm", "
             role, len(rows), med("cycles"), med("clock_ghz"), 100 * med("mfma_util"), med("mfma_flop") / 1e9,
             med("mfma_insts") / 1e6, med("valu_insts") / 1e6, med("trans_insts") / 1e6, 100 * med("valu_busy"),
             rows[0]["vgpr"], rows[0]["agpr"]))
+    return "\n".join(lines)
+
+
+def _mfma_table_i8(by, roles_wanted) -> str:
+    lines = ["| kernel | dispatches | cycles (per XCD) | MFMA busy | int8 MFMA GOP | bf16 MFMA GFLOP | VALU busy |",
+             "|---|---:|---:|---:|---:|---:|---:|"]
+    for role in roles_wanted:
+        rows = by.get(role)
+        if not rows:
+            continue
+        med = lambda k: statistics.median(r[k] for r in rows)
+        lines.append("| `%s` | %d | %.0f | %.1f %% | %.1f | %.1f | %.1f %% |" % (
+            role[:90], len(rows), med("cycles"), 100 * med("mfma_util"), med("mfma_iop") / 1e9,
+            med("mfma_flop") / 1e9, 100 * med("valu_busy")))
     return "\n".join(lines)
 
 
@@ -188,11 +208,12 @@ def main(argv=None):
     q = sub.add_parser("mfma")
     q.add_argument("csv")
     q.add_argument("--simds", type=int, default=1024)
+    q.add_argument("--all", action="store_true", help="every kernel, not only the DiT roles")
     a = ap.parse_args(argv)
     if a.cmd == "stats":
         print(stats(a.csv, a.top))
     elif a.cmd == "mfma":
-        print(mfma_table(mfma(a.csv, a.simds)))
+        print(mfma_table(mfma(a.csv, a.simds), None if a.all else mfma_table.__defaults__[0]))
     else:
         factors, out = pmc(a.fetch_csv, a.write_csv, a.calib_mib)
         table, machine = pmc_table(factors, out)
