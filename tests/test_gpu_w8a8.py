@@ -34,7 +34,7 @@ def test_golden_int8_linear_bit_exact():
     assert torch.equal(y.view(torch.int16), ref.view(torch.int16)), (y.float() - ref.float()).abs().max()
 
 
-@pytest.mark.parametrize("M,K", [(37, 1024), (513, 4096), (4096, 1024)])
+@pytest.mark.parametrize("M,K", [(37, 1024), (513, 4096), (4096, 1024), (5, 2048), (61, 2056), (9, 8)])
 def test_activation_quant_bit_exact(M, K):
     from nanovllm_dots_amd.int8 import quant_act
     rs = np.random.RandomState(M + K)
