@@ -17,8 +17,8 @@
 // semantics): query token j sees keys [0, Lk - Lq + j]. Query head h uses KV
 // head h / G, G = heads / kv_heads.
 //
-// Work split (split-KV): one workgroup = one wave = 32 query rows of one
-// (sequence, KV head) against one chunk of 256 keys (wider past 32 K keys, so
+// Work split (split-KV): one workgroup = one wave = 32 query rows (8 when every
+// sequence has at most 8: decode with a GQA group <= 8) of one (sequence, KV head) against one chunk of 256 keys (wider past 32 K keys, so
 // a row has at most 128 chunks). A row is a (token, head
 // within the group) pair, so at decode one wave serves the G heads that share
 // the KV head, and K / V are read once for all of them. Inside the chunk the
@@ -27,6 +27,7 @@
 // lane), P^T to LDS, then O += P V on the VALU with each lane owning head_dim/64
 // columns of O and reading V rows coalesced (the MFMA operand layout would need
 // V transposed; at <= 32 rows this product is small next to the K / V bytes).
+// In 8-row tiles the next tile's K and V are requested while this tile is computed.
 // Each chunk writes (max, sum, O) per row to the workspace; a combine kernel
 // merges the chunks of a row and writes bf16. Pages are multiples of 256
 // tokens, so a 64-key tile never straddles a page.
@@ -76,15 +77,19 @@ __device__ __forceinline__ long key_row(const PagedParams& a, int i, int t) {
   return (long)a.cu_k[i] + t;
 }
 
-template <int HD>
-constexpr int part_floats() { return 2 * PR + PR * HD; }
+// workspace floats of one (row tile, KV head, chunk) partial of an NR-row tile:
+// max[NR], sum[NR], O[NR][HD]
+template <int HD, int NR>
+constexpr int part_floats() { return 2 * NR + NR * HD; }
 
-template <int HD>
+// NR query rows per workgroup: 32, or 8 when a sequence's tile has at most 8
+// rows (decode with a GQA group <= 8), which keeps O in 16 registers per lane
+template <int HD, int NR>
 __global__ void __launch_bounds__(64) paged_attention_kernel(PagedParams a) {
   constexpr int KK = HD / 16;  // MFMA k-steps over the head dim
   constexpr int DPL = HD / 64; // O columns per lane
-  __shared__ __align__(16) float Ps[PT][PR];  // P^T of the current tile: [key][row]
-  __shared__ __align__(16) float As[PR];      // per-row rescale of O for the current tile
+  __shared__ __align__(16) float Ps[PT][NR];  // P^T of the current tile: [key][row]
+  __shared__ __align__(16) float As[NR];      // per-row rescale of O for the current tile
   const int lane = threadIdx.x, l32 = lane & 31, hi = lane >> 5;
   const int c = blockIdx.x % a.n_chunks;
   const int it = blockIdx.x / a.n_chunks;  // sequence * n_tiles + row tile
@@ -94,22 +99,22 @@ __global__ void __launch_bounds__(64) paged_attention_kernel(PagedParams a) {
   const int Lq = a.cu_q[i + 1] - q0;
   const int Lk = seq_lk(a, i);
   const int G = a.group;
-  const int R = min(PR, Lq * G - tile * PR);  // rows of this tile (uniform)
+  const int R = min(NR, Lq * G - tile * NR);  // rows of this tile (uniform)
   if (R <= 0 || c * a.chunk >= Lk) return;
-  float* part = a.ws + ((long)(it * a.kv_heads + g) * a.n_chunks + c) * part_floats<HD>();
+  float* part = a.ws + ((long)(it * a.kv_heads + g) * a.n_chunks + c) * part_floats<HD, NR>();
   // this lane's row (clamped to the last real row) and its visible-key limit
   const int r_me = min(l32, R - 1);
-  const int gr = tile * PR + r_me;
+  const int gr = tile * NR + r_me;
   const int j = gr / G, gh = gr % G;
   const int lim = a.causal ? min(Lk, Lk - Lq + j + 1) : Lk;
   // the tile's largest limit: chunks beyond it hold no visible key
-  const int j_max = (tile * PR + R - 1) / G;
+  const int j_max = (tile * NR + R - 1) / G;
   const int lim_max = a.causal ? min(Lk, Lk - Lq + j_max + 1) : Lk;
   const int k0 = c * a.chunk;
   if (k0 >= lim_max) {
     if (hi == 0 && l32 < R) {
       part[l32] = -INFINITY;
-      part[PR + l32] = 0.f;
+      part[NR + l32] = 0.f;
     }
     return;
   }
@@ -120,36 +125,61 @@ __global__ void __launch_bounds__(64) paged_attention_kernel(PagedParams a) {
 #pragma unroll
     for (int kk = 0; kk < KK; ++kk) qf[kk] = *reinterpret_cast<const bf16x8*>(qp + 16 * kk);
   }
-  float m_run = -INFINITY, l_run = 0.f;  // row l32's running max / sum (both halves agree)
-  float o[PR][DPL];
+  // In 8-row tiles the K and V of one tile live in registers: the next tile's K
+  // is requested right after this tile's S = K Q^T, its V right after this
+  // tile's P V, and its page is looked up one tile ahead, so a tile waits on one
+  // memory round trip at most. 32-row tiles hold O in 64 registers per lane;
+  // there K is loaded per 32-key block just before its MFMAs and V after them,
+  // which keeps two waves per SIMD.
+  constexpr bool ahead = NR == 8;
+  using VT = typename std::conditional<DPL == 2, uint32_t, uint16_t>::type;
+  bf16x8 kf[ahead ? 2 : 1][KK];  // block kb: keys kb*32 + l32, dims 16*kk + 8*hi .. +8
+  VT vr[PT];                     // key t: this lane's DPL columns
+  auto load_kb = [&](int slot, long row0, int last, int kb) {
+    const int kt = min(kb * 32 + l32, last);  // keys past Lk read the last key (masked)
+    const uint16_t* kp = a.k + (row0 + kt) * a.kv_stride + (long)g * HD + 8 * hi;
 #pragma unroll
-  for (int r = 0; r < PR; ++r)
+    for (int kk = 0; kk < KK; ++kk) kf[slot][kk] = *reinterpret_cast<const bf16x8*>(kp + 16 * kk);
+  };
+  auto load_v = [&](long row0, int last) {
+#pragma unroll
+    for (int t = 0; t < PT; ++t)
+      vr[t] = *reinterpret_cast<const VT*>(a.v + (row0 + min(t, last)) * a.kv_stride + (long)g * HD + DPL * lane);
+  };
+  float m_run = -INFINITY, l_run = 0.f;  // row l32's running max / sum (both halves agree)
+  float o[NR][DPL];
+#pragma unroll
+  for (int r = 0; r < NR; ++r)
 #pragma unroll
     for (int e = 0; e < DPL; ++e) o[r][e] = 0.f;
   const int kend = min(k0 + a.chunk, lim_max);
+  if (ahead) {
+    const long row0 = key_row(a, i, k0);
+    load_kb(0, row0, Lk - 1 - k0, 0);
+    load_kb(ahead ? 1 : 0, row0, Lk - 1 - k0, 1);
+    load_v(row0, Lk - 1 - k0);
+  }
   for (int t0 = k0; t0 < kend; t0 += PT) {
-    const int last = Lk - 1 - t0;  // keys past Lk read the last key (masked)
-    const long row0 = key_row(a, i, t0);
+    const int tn = t0 + PT;
+    const bool more = ahead && tn < kend;  // uniform
+    const long row_n = more ? key_row(a, i, tn) : 0;
+    const long row0 = ahead ? 0 : key_row(a, i, t0);
     // S^T = K Q^T: block kb holds keys t0 + kb*32 + [0, 32)
     floatx16 s[2];
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
       for (int e = 0; e < 16; ++e) s[kb][e] = 0.f;
-      const int kt = min(kb * 32 + l32, last);
-      const uint16_t* kp = a.k + (row0 + kt) * a.kv_stride + (long)g * HD + 8 * hi;
-      bf16x8 kf[KK];
+      if (!ahead) load_kb(0, row0, Lk - 1 - t0, kb);
 #pragma unroll
-      for (int kk = 0; kk < KK; ++kk) kf[kk] = *reinterpret_cast<const bf16x8*>(kp + 16 * kk);
-#pragma unroll
-      for (int kk = 0; kk < KK; ++kk) s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[kk], qf[kk], s[kb], 0, 0, 0);
+      for (int kk = 0; kk < KK; ++kk)
+        s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[ahead ? kb : 0][kk], qf[kk], s[kb], 0, 0, 0);
     }
-    // V columns of this lane for the tile's 64 keys, requested before the softmax
-    using VT = typename std::conditional<DPL == 2, uint32_t, uint16_t>::type;
-    VT vr[PT];
-#pragma unroll
-    for (int t = 0; t < PT; ++t)
-      vr[t] = *reinterpret_cast<const VT*>(a.v + (row0 + min(t, last)) * a.kv_stride + (long)g * HD + DPL * lane);
+    if (more) {
+      load_kb(0, row_n, Lk - 1 - tn, 0);
+      load_kb(ahead ? 1 : 0, row_n, Lk - 1 - tn, 1);
+    }
+    if (!ahead) load_v(row0, Lk - 1 - t0);  // requested before the softmax
     // scores of row l32: lane holds keys kb*32 + 8*(e/4) + 4*hi + e%4
     float mx = -INFINITY;
 #pragma unroll
@@ -172,16 +202,16 @@ __global__ void __launch_bounds__(64) paged_attention_kernel(PagedParams a) {
       for (int e = 0; e < 16; ++e) {
         const float p = exp2f(s[kb][e] - m_use);
         psum += p;
-        Ps[kb * 32 + 8 * (e >> 2) + 4 * hi + (e & 3)][l32] = p;
+        if (NR == 32 || l32 < NR) Ps[kb * 32 + 8 * (e >> 2) + 4 * hi + (e & 3)][l32] = p;
       }
     psum += __shfl_xor(psum, 32, 64);
     l_run = l_run * alpha + psum;
     m_run = m_new;
-    if (hi == 0) As[l32] = alpha;
+    if (hi == 0 && l32 < NR) As[l32] = alpha;
     __syncthreads();
     // O[r][d] = alpha[r] * O[r][d] + sum_t P[r][t] V[t][d], rows in groups of 8
 #pragma unroll
-    for (int rb = 0; rb < PR / 8; ++rb) {
+    for (int rb = 0; rb < NR / 8; ++rb) {
       if (rb * 8 >= R) break;  // uniform
       const float4 a0 = *reinterpret_cast<const float4*>(&As[rb * 8]);
       const float4 a1 = *reinterpret_cast<const float4*>(&As[rb * 8 + 4]);
@@ -208,15 +238,16 @@ __global__ void __launch_bounds__(64) paged_attention_kernel(PagedParams a) {
           for (int e = 0; e < DPL; ++e) o[rb * 8 + r][e] = fmaf(pv[r], vv[e], o[rb * 8 + r][e]);
       }
     }
+    if (more) load_v(row_n, Lk - 1 - tn);
     __syncthreads();  // Ps / As are rewritten by the next tile
   }
   if (hi == 0 && l32 < R) {
     part[l32] = m_run;
-    part[PR + l32] = l_run;
+    part[NR + l32] = l_run;
   }
-  float* po = part + 2 * PR;
+  float* po = part + 2 * NR;
 #pragma unroll
-  for (int r = 0; r < PR; ++r) {
+  for (int r = 0; r < NR; ++r) {
     if (r >= R) break;  // uniform
     if constexpr (DPL == 2) {
       *reinterpret_cast<float2*>(po + r * HD + 2 * lane) = make_float2(o[r][0], o[r][1]);
@@ -232,27 +263,28 @@ __global__ void __launch_bounds__(64) paged_attention_kernel(PagedParams a) {
 // O reads of a thread do not depend on each other, so they are issued back to
 // back. A row that sees no key is 0. At most kMaxChunks chunks per row (the
 // launcher widens chunks to keep it so).
-template <int HD>
+template <int HD, int NR>
 __global__ void __launch_bounds__(256) paged_combine_kernel(PagedParams a) {
-  __shared__ float Ms[PR][kMaxChunks + 1];  // chunk maxima, then weights
-  __shared__ float Ls[PR][kMaxChunks + 1];
+  __shared__ float Ms[NR][kMaxChunks + 1];  // chunk maxima, then weights
+  __shared__ float Ls[NR][kMaxChunks + 1];
   const int it = blockIdx.x, g = blockIdx.y;
   const int i = it / a.n_tiles, tile = it % a.n_tiles;
   const int q0 = a.cu_q[i];
   const int Lq = a.cu_q[i + 1] - q0;
   const int Lk = seq_lk(a, i);
   const int G = a.group;
-  const int R = min(PR, Lq * G - tile * PR);
+  const int R = min(NR, Lq * G - tile * NR);
   if (R <= 0) return;
   // chunks launched for this row (keys past max_k, a caller error, are not seen)
   const int nc = min((Lk + a.chunk - 1) / a.chunk, a.n_chunks);
-  const float* pp = a.ws + (long)(it * a.kv_heads + g) * a.n_chunks * part_floats<HD>();
+  constexpr int PF = part_floats<HD, NR>();
+  const float* pp = a.ws + (long)(it * a.kv_heads + g) * a.n_chunks * PF;
   const int tid = threadIdx.x;
   for (int idx = tid; idx < R * nc; idx += 256) {
     const int r = idx % R, cc = idx / R;
-    const float* p = pp + (long)cc * part_floats<HD>();
+    const float* p = pp + (long)cc * PF;
     Ms[r][cc] = p[r];
-    Ls[r][cc] = p[PR + r];
+    Ls[r][cc] = p[NR + r];
   }
   __syncthreads();
   if (tid < R) {
@@ -268,15 +300,15 @@ __global__ void __launch_bounds__(256) paged_combine_kernel(PagedParams a) {
   __syncthreads();
   for (int e = tid; e < R * HD; e += 256) {
     const int r = e / HD, d = e % HD;
-    const float* po = pp + 2 * PR + r * HD + d;
+    const float* po = pp + 2 * NR + r * HD + d;
     float o = 0.f;
 #pragma unroll 8
     for (int cc = 0; cc < nc; ++cc) {
       const float w = Ms[r][cc];
-      const float x = po[(long)cc * part_floats<HD>()];
+      const float x = po[(long)cc * PF];
       o += w != 0.f ? w * x : 0.f;
     }
-    const int gr = tile * PR + r;
+    const int gr = tile * NR + r;
     const int j = gr / G, gh = gr % G;
     a.out[(long)(q0 + j) * a.out_stride + (long)(g * G + gh) * HD + d] = f2bf(o);
   }
@@ -310,6 +342,7 @@ int chunk_keys(int max_k) {
   return (int)((units + kMaxChunks - 1) / kMaxChunks) * PCH;
 }
 
+// sized for 32-row tiles, which also bounds the 8-row tiles of decode
 long paged_attention_ws_floats(int batch, int kv_heads, int group, int max_q, int max_k, int head_dim) {
   const long n_tiles = ((long)max_q * group + PR - 1) / PR;
   const long n_chunks = ((long)max_k + chunk_keys(max_k) - 1) / chunk_keys(max_k);
@@ -329,7 +362,9 @@ hipError_t paged_attention(const PagedAttnArgs& x, hipStream_t s) {
   a.ws = x.ws;
   a.kv_heads = x.kv_heads;
   a.group = x.heads / x.kv_heads;
-  a.n_tiles = (int)(((long)x.max_q * a.group + PR - 1) / PR);
+  // a tile of 8 rows when every sequence's new rows fit one (decode, GQA group <= 8)
+  const int nr = (long)x.max_q * a.group <= 8 ? 8 : PR;
+  a.n_tiles = (int)(((long)x.max_q * a.group + nr - 1) / nr);
   a.chunk = chunk_keys(x.max_k);
   a.n_chunks = (x.max_k + a.chunk - 1) / a.chunk;
   a.scale_log2 = x.scale * 1.4426950408889634f;
@@ -338,18 +373,18 @@ hipError_t paged_attention(const PagedAttnArgs& x, hipStream_t s) {
   if (items * a.n_chunks > 0x7fffffffL || x.kv_heads > 65535) return hipErrorInvalidValue;
   const dim3 grid((unsigned)(items * a.n_chunks), (unsigned)x.kv_heads);
   const dim3 cgrid((unsigned)items, (unsigned)x.kv_heads);
-  if (x.head_dim == 128) {
-    dfh_launch(paged_attention_kernel<128>, grid, dim3(64), 0, s, a);
+  auto run = [&](auto attn, auto combine) {
+    dfh_launch(attn, grid, dim3(64), 0, s, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(paged_combine_kernel<128>, cgrid, dim3(256), 0, s, a);
-  } else {
-    dfh_launch(paged_attention_kernel<64>, grid, dim3(64), 0, s, a);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(paged_combine_kernel<64>, cgrid, dim3(256), 0, s, a);
-  }
-  return hipGetLastError();
+    hipLaunchKernelGGL(combine, cgrid, dim3(256), 0, s, a);
+    return hipGetLastError();
+  };
+  if (x.head_dim == 128)
+    return nr == 8 ? run(paged_attention_kernel<128, 8>, paged_combine_kernel<128, 8>)
+                   : run(paged_attention_kernel<128, PR>, paged_combine_kernel<128, PR>);
+  return nr == 8 ? run(paged_attention_kernel<64, 8>, paged_combine_kernel<64, 8>)
+                 : run(paged_attention_kernel<64, PR>, paged_combine_kernel<64, PR>);
 }
 
 hipError_t store_kvcache(const uint16_t* key, long key_stride, const uint16_t* value, long value_stride,
