@@ -17,17 +17,18 @@
 // semantics): query token j sees keys [0, Lk - Lq + j]. Query head h uses KV
 // head h / G, G = heads / kv_heads.
 //
-// Work split (split-KV): one workgroup = one wave = 32 query rows (8 when every
-// sequence has at most 8: decode with a GQA group <= 8) of one (sequence, KV head) against one chunk of 256 keys (wider past 32 K keys, so
-// a row has at most 128 chunks). A row is a (token, head
-// within the group) pair, so at decode one wave serves the G heads that share
-// the KV head, and K / V are read once for all of them. Inside the chunk the
-// wave walks four 64-key tiles with an online softmax: S^T = K Q^T on MFMA
-// (32 keys x 32 rows per block, K and Q straight from global memory, 16 B per
-// lane), P^T to LDS, then O += P V on the VALU with each lane owning head_dim/64
-// columns of O and reading V rows coalesced (the MFMA operand layout would need
-// V transposed; at <= 32 rows this product is small next to the K / V bytes).
-// In 8-row tiles the next tile's K and V are requested while this tile is computed.
+// Work split (split-KV): one workgroup = one wave = 32 query rows of one
+// (sequence, KV head) against one chunk of 256 keys (wider past 32 K keys, so
+// a row has at most 128 chunks). A row is a (token, head within the group)
+// pair, so at decode one wave serves the G heads that share the KV head, and
+// K / V are read once for all of them. Inside the chunk the wave walks four
+// 64-key tiles with an online softmax, both products on MFMA:
+//   S^T = K Q^T (32 keys x 32 rows per block, K and Q straight from global
+//   memory, 16 B per lane);
+//   O += P V with P taken from the S registers as the A operand (keys permuted
+//   within each 16-key step, the same way for both operands) and V^T staged in
+//   LDS: each lane loads its columns of every V row (coalesced row reads) and
+//   writes them transposed, 4 keys per 8-B store.
 // Each chunk writes (max, sum, O) per row to the workspace; a combine kernel
 // merges the chunks of a row and writes bf16. Pages are multiples of 256
 // tokens, so a 64-key tile never straddles a page.
@@ -77,19 +78,19 @@ __device__ __forceinline__ long key_row(const PagedParams& a, int i, int t) {
   return (long)a.cu_k[i] + t;
 }
 
-// workspace floats of one (row tile, KV head, chunk) partial of an NR-row tile:
-// max[NR], sum[NR], O[NR][HD]
-template <int HD, int NR>
-constexpr int part_floats() { return 2 * NR + NR * HD; }
+// workspace floats of one (row tile, KV head, chunk) partial: max[PR], sum[PR], O[PR][HD]
+template <int HD>
+constexpr int part_floats() { return 2 * PR + PR * HD; }
 
-// NR query rows per workgroup: 32, or 8 when a sequence's tile has at most 8
-// rows (decode with a GQA group <= 8), which keeps O in 16 registers per lane
-template <int HD, int NR>
-__global__ void __launch_bounds__(64) paged_attention_kernel(PagedParams a) {
+template <int HD>
+__global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) paged_attention_kernel(PagedParams a) {
   constexpr int KK = HD / 16;  // MFMA k-steps over the head dim
-  constexpr int DPL = HD / 64; // O columns per lane
-  __shared__ __align__(16) float Ps[PT][NR];  // P^T of the current tile: [key][row]
-  __shared__ __align__(16) float As[NR];      // per-row rescale of O for the current tile
+  constexpr int DPL = HD / 64; // V columns per lane as loaded
+  // V^T of the current tile (pitch PT + 4 keys: the 8-B operand reads of a
+  // half-wave hit 64 distinct banks) and the per-row rescale of O
+  constexpr int VTP = PT + 4;
+  __shared__ __align__(16) uint16_t Vt[HD][VTP];
+  __shared__ __align__(16) float As[PR];
   const int lane = threadIdx.x, l32 = lane & 31, hi = lane >> 5;
   const int c = blockIdx.x % a.n_chunks;
   const int it = blockIdx.x / a.n_chunks;  // sequence * n_tiles + row tile
@@ -99,22 +100,22 @@ __global__ void __launch_bounds__(64) paged_attention_kernel(PagedParams a) {
   const int Lq = a.cu_q[i + 1] - q0;
   const int Lk = seq_lk(a, i);
   const int G = a.group;
-  const int R = min(NR, Lq * G - tile * NR);  // rows of this tile (uniform)
+  const int R = min(PR, Lq * G - tile * PR);  // rows of this tile (uniform)
   if (R <= 0 || c * a.chunk >= Lk) return;
-  float* part = a.ws + ((long)(it * a.kv_heads + g) * a.n_chunks + c) * part_floats<HD, NR>();
+  float* part = a.ws + ((long)(it * a.kv_heads + g) * a.n_chunks + c) * part_floats<HD>();
   // this lane's row (clamped to the last real row) and its visible-key limit
   const int r_me = min(l32, R - 1);
-  const int gr = tile * NR + r_me;
+  const int gr = tile * PR + r_me;
   const int j = gr / G, gh = gr % G;
   const int lim = a.causal ? min(Lk, Lk - Lq + j + 1) : Lk;
   // the tile's largest limit: chunks beyond it hold no visible key
-  const int j_max = (tile * NR + R - 1) / G;
+  const int j_max = (tile * PR + R - 1) / G;
   const int lim_max = a.causal ? min(Lk, Lk - Lq + j_max + 1) : Lk;
   const int k0 = c * a.chunk;
   if (k0 >= lim_max) {
     if (hi == 0 && l32 < R) {
       part[l32] = -INFINITY;
-      part[NR + l32] = 0.f;
+      part[PR + l32] = 0.f;
     }
     return;
   }
@@ -125,61 +126,37 @@ __global__ void __launch_bounds__(64) paged_attention_kernel(PagedParams a) {
 #pragma unroll
     for (int kk = 0; kk < KK; ++kk) qf[kk] = *reinterpret_cast<const bf16x8*>(qp + 16 * kk);
   }
-  // In 8-row tiles the K and V of one tile live in registers: the next tile's K
-  // is requested right after this tile's S = K Q^T, its V right after this
-  // tile's P V, and its page is looked up one tile ahead, so a tile waits on one
-  // memory round trip at most. 32-row tiles hold O in 64 registers per lane;
-  // there K is loaded per 32-key block just before its MFMAs and V after them,
-  // which keeps two waves per SIMD.
-  constexpr bool ahead = NR == 8;
-  using VT = typename std::conditional<DPL == 2, uint32_t, uint16_t>::type;
-  bf16x8 kf[ahead ? 2 : 1][KK];  // block kb: keys kb*32 + l32, dims 16*kk + 8*hi .. +8
-  VT vr[PT];                     // key t: this lane's DPL columns
-  auto load_kb = [&](int slot, long row0, int last, int kb) {
-    const int kt = min(kb * 32 + l32, last);  // keys past Lk read the last key (masked)
-    const uint16_t* kp = a.k + (row0 + kt) * a.kv_stride + (long)g * HD + 8 * hi;
-#pragma unroll
-    for (int kk = 0; kk < KK; ++kk) kf[slot][kk] = *reinterpret_cast<const bf16x8*>(kp + 16 * kk);
-  };
-  auto load_v = [&](long row0, int last) {
-#pragma unroll
-    for (int t = 0; t < PT; ++t)
-      vr[t] = *reinterpret_cast<const VT*>(a.v + (row0 + min(t, last)) * a.kv_stride + (long)g * HD + DPL * lane);
-  };
   float m_run = -INFINITY, l_run = 0.f;  // row l32's running max / sum (both halves agree)
-  float o[NR][DPL];
+  // O in MFMA layout: block db = columns db*32 + l32, rows 8*(e/4) + 4*hi + e%4
+  floatx16 o[HD / 32];
 #pragma unroll
-  for (int r = 0; r < NR; ++r)
+  for (int db = 0; db < HD / 32; ++db)
 #pragma unroll
-    for (int e = 0; e < DPL; ++e) o[r][e] = 0.f;
+    for (int e = 0; e < 16; ++e) o[db][e] = 0.f;
   const int kend = min(k0 + a.chunk, lim_max);
-  if (ahead) {
-    const long row0 = key_row(a, i, k0);
-    load_kb(0, row0, Lk - 1 - k0, 0);
-    load_kb(ahead ? 1 : 0, row0, Lk - 1 - k0, 1);
-    load_v(row0, Lk - 1 - k0);
-  }
   for (int t0 = k0; t0 < kend; t0 += PT) {
-    const int tn = t0 + PT;
-    const bool more = ahead && tn < kend;  // uniform
-    const long row_n = more ? key_row(a, i, tn) : 0;
-    const long row0 = ahead ? 0 : key_row(a, i, t0);
+    const int last = Lk - 1 - t0;  // keys past Lk read the last key (masked)
+    const long row0 = key_row(a, i, t0);
     // S^T = K Q^T: block kb holds keys t0 + kb*32 + [0, 32)
     floatx16 s[2];
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
       for (int e = 0; e < 16; ++e) s[kb][e] = 0.f;
-      if (!ahead) load_kb(0, row0, Lk - 1 - t0, kb);
+      const int kt = min(kb * 32 + l32, last);
+      const uint16_t* kp = a.k + (row0 + kt) * a.kv_stride + (long)g * HD + 8 * hi;
+      bf16x8 kf[KK];
 #pragma unroll
-      for (int kk = 0; kk < KK; ++kk)
-        s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[ahead ? kb : 0][kk], qf[kk], s[kb], 0, 0, 0);
+      for (int kk = 0; kk < KK; ++kk) kf[kk] = *reinterpret_cast<const bf16x8*>(kp + 16 * kk);
+#pragma unroll
+      for (int kk = 0; kk < KK; ++kk) s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[kk], qf[kk], s[kb], 0, 0, 0);
     }
-    if (more) {
-      load_kb(0, row_n, Lk - 1 - tn, 0);
-      load_kb(ahead ? 1 : 0, row_n, Lk - 1 - tn, 1);
-    }
-    if (!ahead) load_v(row0, Lk - 1 - t0);  // requested before the softmax
+    // V rows of the tile (this lane's DPL columns of each key), requested before the softmax
+    using VT = typename std::conditional<DPL == 2, uint32_t, uint16_t>::type;
+    VT vr[PT];
+#pragma unroll
+    for (int t = 0; t < PT; ++t)
+      vr[t] = *reinterpret_cast<const VT*>(a.v + (row0 + min(t, last)) * a.kv_stride + (long)g * HD + DPL * lane);
     // scores of row l32: lane holds keys kb*32 + 8*(e/4) + 4*hi + e%4
     float mx = -INFINITY;
 #pragma unroll
@@ -202,59 +179,73 @@ __global__ void __launch_bounds__(64) paged_attention_kernel(PagedParams a) {
       for (int e = 0; e < 16; ++e) {
         const float p = exp2f(s[kb][e] - m_use);
         psum += p;
-        if (NR == 32 || l32 < NR) Ps[kb * 32 + 8 * (e >> 2) + 4 * hi + (e & 3)][l32] = p;
+        s[kb][e] = p;
       }
     psum += __shfl_xor(psum, 32, 64);
     l_run = l_run * alpha + psum;
     m_run = m_new;
-    if (hi == 0 && l32 < NR) As[l32] = alpha;
-    __syncthreads();
-    // O[r][d] = alpha[r] * O[r][d] + sum_t P[r][t] V[t][d], rows in groups of 8
+    if (hi == 0) As[l32] = alpha;
+    // V^T[d][t] of the tile: this lane's columns DPL*lane + cc, 4 keys per 8-B write
 #pragma unroll
-    for (int rb = 0; rb < NR / 8; ++rb) {
-      if (rb * 8 >= R) break;  // uniform
-      const float4 a0 = *reinterpret_cast<const float4*>(&As[rb * 8]);
-      const float4 a1 = *reinterpret_cast<const float4*>(&As[rb * 8 + 4]);
-      const float av[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+    for (int t = 0; t < PT; t += 4)
 #pragma unroll
-      for (int r = 0; r < 8; ++r)
-#pragma unroll
-        for (int e = 0; e < DPL; ++e) o[rb * 8 + r][e] *= av[r];
-#pragma unroll 8
-      for (int t = 0; t < PT; ++t) {
-        const float4 p0 = *reinterpret_cast<const float4*>(&Ps[t][rb * 8]);
-        const float4 p1 = *reinterpret_cast<const float4*>(&Ps[t][rb * 8 + 4]);
-        const float pv[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
-        float vv[DPL];
+      for (int cc = 0; cc < DPL; ++cc) {
+        uint32_t w0, w1;
         if constexpr (DPL == 2) {
-          vv[0] = __uint_as_float(vr[t] << 16);
-          vv[1] = __uint_as_float(vr[t] & 0xffff0000u);
+          const uint32_t sel = cc ? 0x07060302u : 0x05040100u;  // high / low halves of two keys
+          w0 = __builtin_amdgcn_perm(vr[t + 1], vr[t], sel);
+          w1 = __builtin_amdgcn_perm(vr[t + 3], vr[t + 2], sel);
         } else {
-          vv[0] = bf2f(vr[t]);
+          w0 = (uint32_t)vr[t] | ((uint32_t)vr[t + 1] << 16);
+          w1 = (uint32_t)vr[t + 2] | ((uint32_t)vr[t + 3] << 16);
         }
+        *reinterpret_cast<uint2*>(&Vt[DPL * lane + cc][t]) = make_uint2(w0, w1);
+      }
+    __syncthreads();
+    // O = alpha * O + P V on MFMA. k-step q covers the 16 keys that this lane's
+    // S entries e = 8*(q%2) .. +8 of block q/2 hold: for half hi, keys
+    // 32*(q/2) + 16*(q%2) + 4*hi + {0..3, 8..11}. The V^T operand takes the same keys.
 #pragma unroll
-        for (int r = 0; r < 8; ++r)
+    for (int g4 = 0; g4 < 4; ++g4) {
+      const float4 al = *reinterpret_cast<const float4*>(&As[8 * g4 + 4 * hi]);
 #pragma unroll
-          for (int e = 0; e < DPL; ++e) o[rb * 8 + r][e] = fmaf(pv[r], vv[e], o[rb * 8 + r][e]);
+      for (int db = 0; db < HD / 32; ++db) {
+        o[db][4 * g4 + 0] *= al.x;
+        o[db][4 * g4 + 1] *= al.y;
+        o[db][4 * g4 + 2] *= al.z;
+        o[db][4 * g4 + 3] *= al.w;
       }
     }
-    if (more) load_v(row_n, Lk - 1 - tn);
-    __syncthreads();  // Ps / As are rewritten by the next tile
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int kb = q >> 1, e0 = 8 * (q & 1);
+      const uint4 pw = make_uint4(pack2(s[kb][e0], s[kb][e0 + 1]), pack2(s[kb][e0 + 2], s[kb][e0 + 3]),
+                                  pack2(s[kb][e0 + 4], s[kb][e0 + 5]), pack2(s[kb][e0 + 6], s[kb][e0 + 7]));
+      const bf16x8 pa = __builtin_bit_cast(bf16x8, pw);
+      const int kq = 32 * kb + 16 * (q & 1) + 4 * hi;
+#pragma unroll
+      for (int db = 0; db < HD / 32; ++db) {
+        const uint16_t* vp = &Vt[db * 32 + l32][kq];
+        const uint2 v0 = *reinterpret_cast<const uint2*>(vp);
+        const uint2 v1 = *reinterpret_cast<const uint2*>(vp + 8);
+        const bf16x8 vb = __builtin_bit_cast(bf16x8, make_uint4(v0.x, v0.y, v1.x, v1.y));
+        o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(pa, vb, o[db], 0, 0, 0);
+      }
+    }
+    __syncthreads();  // Vt / As are rewritten by the next tile
   }
   if (hi == 0 && l32 < R) {
     part[l32] = m_run;
-    part[NR + l32] = l_run;
+    part[PR + l32] = l_run;
   }
-  float* po = part + 2 * NR;
+  float* po = part + 2 * PR;
 #pragma unroll
-  for (int r = 0; r < NR; ++r) {
-    if (r >= R) break;  // uniform
-    if constexpr (DPL == 2) {
-      *reinterpret_cast<float2*>(po + r * HD + 2 * lane) = make_float2(o[r][0], o[r][1]);
-    } else {
-      po[r * HD + lane] = o[r][0];
+  for (int db = 0; db < HD / 32; ++db)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const int r = 8 * (e >> 2) + 4 * hi + (e & 3);
+      if (r < R) po[r * HD + db * 32 + l32] = o[db][e];
     }
-  }
 }
 
 // Merge the chunks of each row: O = sum_c 2^(m_c - M) O_c / sum_c 2^(m_c - M) l_c.
@@ -263,28 +254,28 @@ __global__ void __launch_bounds__(64) paged_attention_kernel(PagedParams a) {
 // O reads of a thread do not depend on each other, so they are issued back to
 // back. A row that sees no key is 0. At most kMaxChunks chunks per row (the
 // launcher widens chunks to keep it so).
-template <int HD, int NR>
+template <int HD>
 __global__ void __launch_bounds__(256) paged_combine_kernel(PagedParams a) {
-  __shared__ float Ms[NR][kMaxChunks + 1];  // chunk maxima, then weights
-  __shared__ float Ls[NR][kMaxChunks + 1];
+  __shared__ float Ms[PR][kMaxChunks + 1];  // chunk maxima, then weights
+  __shared__ float Ls[PR][kMaxChunks + 1];
   const int it = blockIdx.x, g = blockIdx.y;
   const int i = it / a.n_tiles, tile = it % a.n_tiles;
   const int q0 = a.cu_q[i];
   const int Lq = a.cu_q[i + 1] - q0;
   const int Lk = seq_lk(a, i);
   const int G = a.group;
-  const int R = min(NR, Lq * G - tile * NR);
+  const int R = min(PR, Lq * G - tile * PR);
   if (R <= 0) return;
   // chunks launched for this row (keys past max_k, a caller error, are not seen)
   const int nc = min((Lk + a.chunk - 1) / a.chunk, a.n_chunks);
-  constexpr int PF = part_floats<HD, NR>();
+  constexpr int PF = part_floats<HD>();
   const float* pp = a.ws + (long)(it * a.kv_heads + g) * a.n_chunks * PF;
   const int tid = threadIdx.x;
   for (int idx = tid; idx < R * nc; idx += 256) {
     const int r = idx % R, cc = idx / R;
     const float* p = pp + (long)cc * PF;
     Ms[r][cc] = p[r];
-    Ls[r][cc] = p[NR + r];
+    Ls[r][cc] = p[PR + r];
   }
   __syncthreads();
   if (tid < R) {
@@ -300,7 +291,7 @@ __global__ void __launch_bounds__(256) paged_combine_kernel(PagedParams a) {
   __syncthreads();
   for (int e = tid; e < R * HD; e += 256) {
     const int r = e / HD, d = e % HD;
-    const float* po = pp + 2 * NR + r * HD + d;
+    const float* po = pp + 2 * PR + r * HD + d;
     float o = 0.f;
 #pragma unroll 8
     for (int cc = 0; cc < nc; ++cc) {
@@ -308,7 +299,7 @@ __global__ void __launch_bounds__(256) paged_combine_kernel(PagedParams a) {
       const float x = po[(long)cc * PF];
       o += w != 0.f ? w * x : 0.f;
     }
-    const int gr = tile * NR + r;
+    const int gr = tile * PR + r;
     const int j = gr / G, gh = gr % G;
     a.out[(long)(q0 + j) * a.out_stride + (long)(g * G + gh) * HD + d] = f2bf(o);
   }
@@ -342,7 +333,6 @@ int chunk_keys(int max_k) {
   return (int)((units + kMaxChunks - 1) / kMaxChunks) * PCH;
 }
 
-// sized for 32-row tiles, which also bounds the 8-row tiles of decode
 long paged_attention_ws_floats(int batch, int kv_heads, int group, int max_q, int max_k, int head_dim) {
   const long n_tiles = ((long)max_q * group + PR - 1) / PR;
   const long n_chunks = ((long)max_k + chunk_keys(max_k) - 1) / chunk_keys(max_k);
@@ -362,9 +352,7 @@ hipError_t paged_attention(const PagedAttnArgs& x, hipStream_t s) {
   a.ws = x.ws;
   a.kv_heads = x.kv_heads;
   a.group = x.heads / x.kv_heads;
-  // a tile of 8 rows when every sequence's new rows fit one (decode, GQA group <= 8)
-  const int nr = (long)x.max_q * a.group <= 8 ? 8 : PR;
-  a.n_tiles = (int)(((long)x.max_q * a.group + nr - 1) / nr);
+  a.n_tiles = (int)(((long)x.max_q * a.group + PR - 1) / PR);
   a.chunk = chunk_keys(x.max_k);
   a.n_chunks = (x.max_k + a.chunk - 1) / a.chunk;
   a.scale_log2 = x.scale * 1.4426950408889634f;
@@ -380,11 +368,8 @@ hipError_t paged_attention(const PagedAttnArgs& x, hipStream_t s) {
     hipLaunchKernelGGL(combine, cgrid, dim3(256), 0, s, a);
     return hipGetLastError();
   };
-  if (x.head_dim == 128)
-    return nr == 8 ? run(paged_attention_kernel<128, 8>, paged_combine_kernel<128, 8>)
-                   : run(paged_attention_kernel<128, PR>, paged_combine_kernel<128, PR>);
-  return nr == 8 ? run(paged_attention_kernel<64, 8>, paged_combine_kernel<64, 8>)
-                 : run(paged_attention_kernel<64, PR>, paged_combine_kernel<64, PR>);
+  return x.head_dim == 128 ? run(paged_attention_kernel<128>, paged_combine_kernel<128>)
+                           : run(paged_attention_kernel<64>, paged_combine_kernel<64>);
 }
 
 hipError_t store_kvcache(const uint16_t* key, long key_stride, const uint16_t* value, long value_stride,
