@@ -45,6 +45,7 @@ constexpr int PCH = 256;  // keys per chunk unit (a chunk is a multiple of it)
 constexpr int kMaxChunks = 128;  // chunks per row at most (the chunk widens past 32 K keys)
 constexpr int PT = 64;    // keys per tile
 constexpr int PR = 32;    // query rows per workgroup
+constexpr int kCombineSplit = 4;  // column slices of head_dim per combine row tile
 
 struct PagedParams {
   const uint16_t* q;
@@ -253,7 +254,9 @@ __global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) pa
 // sum is loaded once, in parallel, into LDS and turned into a weight there; the
 // O reads of a thread do not depend on each other, so they are issued back to
 // back. A row that sees no key is 0. At most kMaxChunks chunks per row (the
-// launcher widens chunks to keep it so).
+// launcher widens chunks to keep it so). blockIdx.z takes one of kCombineSplit
+// column slices of head_dim (each slice recomputes the few weights), so a
+// decode of a few dozen sequences still fills the GPU.
 template <int HD>
 __global__ void __launch_bounds__(256) paged_combine_kernel(PagedParams a) {
   __shared__ float Ms[PR][kMaxChunks + 1];  // chunk maxima, then weights
@@ -289,8 +292,9 @@ __global__ void __launch_bounds__(256) paged_combine_kernel(PagedParams a) {
       Ms[tid][cc] = (L > 0.f && Ms[tid][cc] != -INFINITY) ? exp2f(Ms[tid][cc] - M) / L : 0.f;
   }
   __syncthreads();
-  for (int e = tid; e < R * HD; e += 256) {
-    const int r = e / HD, d = e % HD;
+  constexpr int CW = HD / kCombineSplit;  // columns of this workgroup
+  for (int e = tid; e < R * CW; e += 256) {
+    const int r = e / CW, d = blockIdx.z * CW + e % CW;
     const float* po = pp + 2 * PR + r * HD + d;
     float o = 0.f;
 #pragma unroll 8
@@ -360,7 +364,7 @@ hipError_t paged_attention(const PagedAttnArgs& x, hipStream_t s) {
   const long items = (long)x.batch * a.n_tiles;
   if (items * a.n_chunks > 0x7fffffffL || x.kv_heads > 65535) return hipErrorInvalidValue;
   const dim3 grid((unsigned)(items * a.n_chunks), (unsigned)x.kv_heads);
-  const dim3 cgrid((unsigned)items, (unsigned)x.kv_heads);
+  const dim3 cgrid((unsigned)items, (unsigned)x.kv_heads, kCombineSplit);
   auto run = [&](auto attn, auto combine) {
     dfh_launch(attn, grid, dim3(64), 0, s, a);
     hipError_t e = hipGetLastError();
