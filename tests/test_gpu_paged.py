@@ -49,7 +49,10 @@ def _cu(lens):
     return torch.tensor([0] + torch.tensor(lens).cumsum(0).tolist(), dtype=torch.int32)
 
 
-@pytest.mark.parametrize("H,Hkv,hd", [(12, 2, 128), (16, 16, 64), (8, 2, 64), (12, 3, 128)])
+# GQA groups 6, 1, 4, 4, 16 and 40: a decode row tile holds 32 (token, head) rows,
+# so the last two fill half a tile and two tiles (32 + 8 rows)
+@pytest.mark.parametrize("H,Hkv,hd", [(12, 2, 128), (16, 16, 64), (8, 2, 64), (12, 3, 128), (32, 2, 128),
+                                      (40, 1, 64)])
 def test_decode_paged_matches_oracle(H, Hkv, hd):
     from nanovllm_dots_amd.paged_attention import flash_attn_with_kvcache
     lens = [1, 255, 256, 257, 700, 1500, 3001]
