@@ -57,11 +57,80 @@ def pmc_traffic(role: str):
     return found.get(role)
 
 
-def cpu_baseline(cfg, W, lens, hist, noise, budget_s: float):
+def host_cpu():
+    """The host's CPU as this process sees it: os.cpu_count(), the CPUs it may run
+    on (affinity), the cgroup CPU quota, lscpu's model name, and the thread count
+    used for the baseline (affinity, capped by the quota: more threads than the
+    quota only time-slice)."""
+    import subprocess
+    info = {"os_cpu_count": os.cpu_count()}
+    try:
+        aff = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        aff = os.cpu_count() or 1
+    info["affinity_cpus"] = aff
+    quota = None
+    try:
+        q, per = open("/sys/fs/cgroup/cpu.max").read().split()[:2]
+        if q != "max":
+            quota = int(q) / int(per)
+    except (OSError, ValueError):
+        pass
+    info["cgroup_cpu_quota"] = quota
+    model = None
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            if line.startswith("Model name:"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except (OSError, subprocess.SubprocessError):
+        pass
+    info["lscpu_model"] = model
+    info["omp_num_threads_env"] = os.environ.get("OMP_NUM_THREADS")
+    threads = aff if quota is None else max(1, min(aff, int(quota)))
+    info["threads_used"] = threads
+    return info
+
+
+def cpu_c1_block(threads: int, warmup: int = 3, runs: int = 10):
+    """C1 on the host: one DiT block (hidden 1024, 16 x 64 heads, MLP 4096) in
+    float32 over 64 context + 16 latent rows, t = dt = 0.25, seed 0 (the oracle's
+    DiTBlock, the computation tests/golden/c1_block.npz pins). Median of ``runs``
+    timed runs after ``warmup``; GFLOP/s of the block's GEMMs (25,165,824 FLOP
+    per row)."""
+    import numpy as np
+    import torch
+    from oracle import dit_ref as R
+    torch.set_num_threads(threads)
+    cfg = R.DitConfig(hidden=1024, heads=16, ffn=4096, n_blocks=1, latent_dim=64, patch=16)
+    W = R.random_dit_weights(cfg, 0)
+    rs = np.random.RandomState(0)
+    x = torch.from_numpy(rs.standard_normal((1, 80, 1024)).astype(np.float32))
+    mask = R.build_fm_attn_mask(64, 80, 16)[None]
+    pos = R.build_fm_pos_ids(64, 80, 16)[None]
+    t = torch.full((1,), 0.25)
+    Rg = R._R("fp32")
+    with torch.no_grad():
+        c = R.condition(W, cfg, t, t, torch.zeros(1, 1024), Rg)
+        h = Rg.linear(x, W["input_layer.weight"], W["input_layer.bias"])
+        times = []
+        for i in range(warmup + runs):
+            t0 = time.perf_counter()
+            R.block_forward_padded(W, cfg, 0, h, c, mask, pos, Rg)
+            if i >= warmup:
+                times.append(time.perf_counter() - t0)
+    times.sort()
+    med = times[len(times) // 2]
+    flops = 25_165_824 * 80
+    return {"gflops": round(flops / med / 1e9, 2), "median_ms": round(med * 1e3, 3), "runs": runs,
+            "warmup": warmup, "threads": threads, "block_gemm_gflop": round(flops / 1e9, 3)}
+
+
+def cpu_baseline(cfg, W, lens, hist, noise, budget_s: float, threads: int):
     """Oracle fp32 MeanFlow solve of the first k requests on the host cores."""
     import torch
     from oracle import dit_ref as R
-    threads = min(os.cpu_count() or 1, 16)
     torch.set_num_threads(threads)
     k = 1
     samples = []
@@ -70,7 +139,8 @@ def cpu_baseline(cfg, W, lens, hist, noise, budget_s: float):
         sub = hist[:k]
         inp, mask, pos, g = R.pack_fm_inputs(sub, cfg.patch, cfg.hidden)
         t0 = time.perf_counter()
-        R.meanflow_solve_varlen(W, cfg, sub, g, noise[:k], 4, "fp32")
+        with torch.no_grad():
+            R.meanflow_solve_varlen(W, cfg, sub, g, noise[:k], 4, "fp32")
         dt = time.perf_counter() - t0
         t_spent += dt
         M = sum(L + cfg.patch for L in lens[:k])
@@ -371,9 +441,13 @@ def main():
     w8 = None if args.no_w8a8 else w8a8_bench()
     kvc = None if args.no_kvcache else kvcache_bench(head, cfg)
 
-    cpu = None
+    cpu = c1 = host = None
     if not args.no_cpu:
-        cpu = cpu_baseline(cfg, W, lens, hist, noise, args.cpu_budget)
+        host = host_cpu()
+        log(f"host cpu: {host}")
+        c1 = cpu_c1_block(host["threads_used"])
+        log(f"cpu c1 block: {c1}")
+        cpu = cpu_baseline(cfg, W, lens, hist, noise, args.cpu_budget, host["threads_used"])
 
     rec = {
         "metric": "DiT GEMM TFLOPS (% MFMA peak) + latent xRT at 64 streams, NFE=4",
@@ -406,6 +480,9 @@ def main():
         "cpu_baseline": ({k: (round(v, 5) if isinstance(v, float) else v) for k, v in cpu.items()
                           if k in ("value", "unit", "cores", "kind", "sample")} if cpu else None),
         "cpu_xRT": round(cpu["xRT"], 4) if cpu else None,
+        "cpu_c1_block_fp32": c1,
+        "cpu_host": dict(host, torch=torch.__version__, mkldnn=torch.backends.mkldnn.is_available())
+        if host else None,
     }
     print(json.dumps(rec), flush=True)
 

@@ -1133,6 +1133,11 @@ int dfh_kvcache_create(DfhHandle* h, int n_streams, int capacity, int num_steps,
   if (n_streams <= 0 || n_streams > 1024 || num_steps <= 0 || num_steps > kMaxTimeVals)
     return fail("dfh_kvcache_create: bad n_streams=%d num_steps=%d", n_streams, num_steps);
   if (capacity < h->cfg.patch + 2) return fail("dfh_kvcache_create: capacity %d too small", capacity);
+  // the decode attention and its chunk merge hold the 1 + P active queries of a
+  // stream in one 32-row MFMA block
+  if (h->cfg.patch + 1 > 32)
+    return fail("dfh_kvcache_create: latent patch %d too large (1 + patch active rows must be <= 32)",
+                h->cfg.patch);
   const int cap = (capacity + 7) & ~7;  // region starts stay 16-byte aligned in V^T
   if ((long)num_steps * n_streams * cap * 2 * h->cfg.hidden >= (1L << 31))
     return fail("dfh_kvcache_create: cache too large for 32-bit offsets");

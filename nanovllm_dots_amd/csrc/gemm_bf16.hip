@@ -809,13 +809,26 @@ gemm_mfma_kernel(GemmArgs a) {
                           __builtin_bit_cast(float, e2), __builtin_bit_cast(float, e3));
         }
   }
+  // The pieces of a tile are dealt to workgroups xcd, xcd + 8, ...: with the
+  // round-robin dispatch of the 8-XCD partition mode they share one L2, where a
+  // piece's stores (acknowledged before it counts itself in) are visible to the
+  // last arriver's loads. A piece that finds itself on another XCD (hardware
+  // register XCC_ID) writes its partial sums back with an agent-scope release
+  // fence and marks the tile (counter bits 16..31); the last arriver of a marked
+  // tile takes an agent-scope acquire fence before reading the pieces.
+  const bool on_xcd = __builtin_amdgcn_s_getreg((3 << 11) | 20) == xcd;  // hwreg(XCC_ID, 0, 4); uniform
+  if (!on_xcd) __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's partial sums are in L2
   __syncthreads();                                   // ... and every wave's; LDS reads done too
   unsigned* cnt = reinterpret_cast<unsigned*>(a.ws) + xcd * per_xcd + tt;
-  if (tid == 0) s_flag = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-                         (unsigned)(split - 1);
+  if (tid == 0) {
+    const unsigned add = on_xcd ? 1u : 0x10001u;
+    const unsigned now = __hip_atomic_fetch_add(cnt, add, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + add;
+    s_flag = (now & 0xffffu) != (unsigned)split ? 0 : (now >> 16) ? 2 : 1;
+  }
   __syncthreads();
   if (!s_flag) return;  // uniform
+  if (s_flag == 2) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
   asm volatile("" ::: "memory");
   if (tid == 0) *cnt = 0u;  // ready for the next launch
   // Last piece in: sum the pieces in piece order, ((p0 + p1) + p2) + ..., the

@@ -6,14 +6,21 @@ pages):
 
 * ``store_kvcache(key, value, k_cache, v_cache, slot_mapping)`` — same
   signature and checks as attention.py:36-47 (the Triton kernel :10-33).
-* ``flash_attn_varlen_func(q, k, v, max_seqlen_q, cu_seqlens_q, max_seqlen_k,
-  cu_seqlens_k, softmax_scale=None, causal=False, block_table=None)`` — the
-  prefill / chunked-append call of attention.py:75-86 (flash-attn 2.8.3
-  argument names and meaning; bottom-right causal alignment).
-* ``flash_attn_with_kvcache(q, k_cache, v_cache, cache_seqlens=None,
-  block_table=None, softmax_scale=None, causal=False)`` — the decode call of
-  attention.py:88-95 (``k``/``v`` appends are not supported: the engine stores
-  K/V with ``store_kvcache`` first).
+* ``flash_attn_varlen_func(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q,
+  max_seqlen_k, dropout_p=0.0, softmax_scale=None, causal=False, ...,
+  block_table=None)`` — the prefill / chunked-append call of attention.py:75-86
+  (flash-attn 2.8.3 positional order, argument names and meaning; bottom-right
+  causal alignment).
+* ``flash_attn_with_kvcache(q, k_cache, v_cache, k=None, v=None,
+  rotary_cos=None, rotary_sin=None, cache_seqlens=None, cache_batch_idx=None,
+  cache_leftpad=None, block_table=None, softmax_scale=None, causal=False, ...)``
+  — the decode call of attention.py:88-95, in flash-attn 2.8.3's positional
+  order (``k``/``v`` appends are not supported: the engine stores K/V with
+  ``store_kvcache`` first).
+
+Options that do not change the result are accepted at any value
+(``num_splits``, a scheduling hint; ``rotary_interleaved`` without rotary
+tables); the others only at their defaults.
 
 Switching the reference to these is an import change in
 ``layers/attention.py``. bf16 only; head_dim 64 or 128; pages a multiple of
@@ -27,19 +34,14 @@ import torch
 
 from . import _lib
 
-_UNSUPPORTED = ("dropout_p", "window_size", "alibi_slopes", "softcap", "return_attn_probs",
-                "deterministic", "rotary_cos", "rotary_sin", "cache_batch_idx", "cache_leftpad")
-
-
-def _check_unsupported(kw):
+def _check_unsupported(**kw):
+    """Options of flash-attn 2.8.3 this path implements only at their defaults."""
     for name, val in kw.items():
-        if name not in _UNSUPPORTED:
-            raise TypeError(f"unexpected argument {name!r}")
         if name == "window_size" and tuple(val) == (-1, -1):
             continue
         if name in ("dropout_p", "softcap") and not val:
             continue
-        if name in ("return_attn_probs", "deterministic") and not val:
+        if name in ("return_attn_probs", "deterministic", "return_softmax_lse") and not val:
             continue
         if val is None:
             continue
@@ -105,24 +107,30 @@ def _run(q, k, v, *, cu_q, max_q, max_k, cu_k=None, seqlens_k=None, block_table=
     return out
 
 
-def flash_attn_varlen_func(q, k, v, max_seqlen_q, cu_seqlens_q, max_seqlen_k, cu_seqlens_k, softmax_scale=None,
-                           causal=False, block_table=None, **kw):
+def flash_attn_varlen_func(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, dropout_p=0.0,
+                           softmax_scale=None, causal=False, window_size=(-1, -1), softcap=0.0, alibi_slopes=None,
+                           deterministic=False, return_attn_probs=False, block_table=None):
     """out [total_q, H, hd]. With ``block_table``, k / v are the paged caches
     [num_blocks, block_size, H_kv, hd] and ``cu_seqlens_k`` gives key counts."""
-    _check_unsupported(kw)
+    _check_unsupported(dropout_p=dropout_p, window_size=window_size, softcap=softcap, alibi_slopes=alibi_slopes,
+                       deterministic=deterministic, return_attn_probs=return_attn_probs)
     bs = k.shape[1] if block_table is not None else 0
     return _run(q, k, v, cu_q=cu_seqlens_q, max_q=max_seqlen_q, max_k=max_seqlen_k, cu_k=cu_seqlens_k,
                 block_table=block_table, block_size=bs, scale=softmax_scale, causal=causal)
 
 
-def flash_attn_with_kvcache(q, k_cache, v_cache, k=None, v=None, cache_seqlens=None, block_table=None,
-                            softmax_scale=None, causal=False, **kw):
+def flash_attn_with_kvcache(q, k_cache, v_cache, k=None, v=None, rotary_cos=None, rotary_sin=None,
+                            cache_seqlens=None, cache_batch_idx=None, cache_leftpad=None, block_table=None,
+                            softmax_scale=None, causal=False, window_size=(-1, -1), softcap=0.0,
+                            rotary_interleaved=True, alibi_slopes=None, num_splits=0, return_softmax_lse=False):
     """q [B, Lq, H, hd] -> out [B, Lq, H, hd] over the first ``cache_seqlens[b]``
     keys of each batch row (paged through ``block_table``, else k_cache
     [B, S, H_kv, hd])."""
     if k is not None or v is not None:
         raise NotImplementedError("k / v appends: store them with store_kvcache first")
-    _check_unsupported(kw)
+    _check_unsupported(rotary_cos=rotary_cos, rotary_sin=rotary_sin, cache_batch_idx=cache_batch_idx,
+                       cache_leftpad=cache_leftpad, window_size=window_size, softcap=softcap,
+                       alibi_slopes=alibi_slopes, return_softmax_lse=return_softmax_lse)
     B, Lq, H, hd = q.shape
     dev = q.device
     if cache_seqlens is None:

@@ -25,7 +25,10 @@ Two numeric regimes:
            Weights are bf16 values (the caller rounds them once).
 
 Tensors passed in and out are float32 holding the regime's values. All
-functions are device-agnostic torch code; tests run them on the CPU.
+functions are device-agnostic torch code. Tests run them on the CPU; the GPU
+parity cases too large for the host (tens of thousands of rows) run the fp32
+regime with torch's own float32 kernels on the GPU, never a kernel of the
+library under test.
 """
 from __future__ import annotations
 
@@ -431,9 +434,11 @@ def fm_key_limit(r: int, c: int, patch: int, hidden_patch_size: int = 1) -> int:
 
 def attention_varlen(W, cfg: DitConfig, l: int, x, lens: list[int], R: _R):
     """MultiHeadAttention.forward on packed rows; request i occupies
-    rows [cu_i, cu_i + c_i + P) with positions 0..c_i+P-1."""
+    rows [cu_i, cu_i + c_i + P) with positions 0..c_i+P-1. Runs on x's device;
+    the score and value products are float32 matmuls of contiguous operands."""
     p = f"blocks.{l}.attn."
     M, H = x.shape
+    dev = x.device
     nh, hd, P = cfg.heads, cfg.head_dim, cfg.patch
     q = R.linear(x, W[p + "q_proj.weight"], W.get(p + "q_proj.bias")).view(M, nh, hd)
     k = R.linear(x, W[p + "k_proj.weight"], W.get(p + "k_proj.bias")).view(M, nh, hd)
@@ -441,22 +446,26 @@ def attention_varlen(W, cfg: DitConfig, l: int, x, lens: list[int], R: _R):
     if cfg.qk_norm != "none":
         q = qk_norm(q, W, p + "q_norm", cfg)
         k = qk_norm(k, W, p + "k_norm", cfg)
-    out = torch.empty(M, nh, hd)
+    out = torch.empty(M, nh, hd, device=dev)
     off = 0
     for c in lens:
         Ti = c + P
         qi, ki, vi = q[off:off + Ti], k[off:off + Ti], v[off:off + Ti]
         if cfg.rotary:
-            cos, sin = rope_tables(torch.arange(Ti, dtype=torch.float32), hd, cfg.rotary_theta)
+            cos, sin = rope_tables(torch.arange(Ti, dtype=torch.float32, device=dev), hd, cfg.rotary_theta)
             qi = apply_rope(qi, cos[:, None], sin[:, None])
             ki = apply_rope(ki, cos[:, None], sin[:, None])
         qi, ki, vi = R.r(qi), R.r(ki), R.r(vi)
-        s = torch.einsum("qhd,khd->hqk", qi.float(), ki.float()) * (hd ** -0.5)
-        lim = torch.tensor([fm_key_limit(r, c, P) for r in range(Ti)])
-        allowed = torch.arange(Ti)[None, :] < lim[:, None]
+        qh = qi.float().permute(1, 0, 2).contiguous()          # [h, q, d]
+        kt = ki.float().permute(1, 2, 0).contiguous()          # [h, d, k]
+        s = torch.matmul(qh, kt) * (hd ** -0.5)
+        r = torch.arange(Ti, device=dev)
+        lim = torch.where(r < c - 1, r + 1, torch.full_like(r, c + P))   # fm_key_limit per row
+        allowed = r[None, :] < lim[:, None]
         s = s.masked_fill(~allowed[None], float("-inf"))
         a = torch.softmax(s, dim=-1)
-        out[off:off + Ti] = R.r(torch.einsum("hqk,khd->qhd", a, vi.float()))
+        o = torch.matmul(a, vi.float().permute(1, 0, 2).contiguous())   # [h, q, d]
+        out[off:off + Ti] = R.r(o.permute(1, 0, 2))
         off += Ti
     return R.linear(out.reshape(M, H), W[p + "o_proj.weight"], W[p + "o_proj.bias"])
 
@@ -468,7 +477,7 @@ def dit_forward_varlen(W, cfg: DitConfig, x, lens: list[int], timesteps, duratio
     R = _R(regime)
     H, P = cfg.hidden, cfg.patch
     c = condition(W, cfg, timesteps, duration, g_cond, R)            # [N, H]
-    row_req = torch.cat([torch.full((ci + P,), i, dtype=torch.long) for i, ci in enumerate(lens)])
+    row_req = torch.cat([torch.full((ci + P,), i, dtype=torch.long) for i, ci in enumerate(lens)]).to(x.device)
     h = R.linear(x, W["input_layer.weight"], W["input_layer.bias"])
     for l in range(cfg.n_blocks):
         p = f"blocks.{l}."
@@ -487,10 +496,12 @@ def dit_forward_varlen(W, cfg: DitConfig, x, lens: list[int], timesteps, duratio
 def meanflow_solve_varlen(W, cfg: DitConfig, histories: list[torch.Tensor], g_cond, noise,
                           num_steps: int = 4, regime: str = "fp32"):
     """The MeanFlow solve on packed rows; equal to ``meanflow_solve`` on the
-    padded layout of the same requests (padding transparency)."""
+    padded layout of the same requests (padding transparency). Runs on the
+    device of ``noise`` (weights, histories and g_cond must live there too)."""
     R = _R(regime)
     P = cfg.patch
     n = len(histories)
+    dev = noise.device
     lens = [h.shape[0] for h in histories]
     ts, dts = meanflow_grid(num_steps, regime)
     z = noise.float()
@@ -499,14 +510,14 @@ def meanflow_solve_varlen(W, cfg: DitConfig, histories: list[torch.Tensor], g_co
     for ci in lens:
         patch_rows.append(torch.arange(off + ci, off + ci + P))
         off += ci + P
-    patch_rows = torch.cat(patch_rows)
-    base = torch.cat([torch.cat([h.float(), torch.zeros(P, h.shape[1])]) for h in histories])
+    patch_rows = torch.cat(patch_rows).to(dev)
+    base = torch.cat([torch.cat([h.float(), torch.zeros(P, h.shape[1], device=dev)]) for h in histories])
     for s in range(num_steps):
         zp = R.linear(z, W["coordinate_proj.weight"], W["coordinate_proj.bias"])
         xs = base.clone()
         xs[patch_rows] = zp.reshape(n * P, -1)
-        v = dit_forward_varlen(W, cfg, xs, lens, torch.full((n,), ts[s]), torch.full((n,), dts[s]),
-                               g_cond, regime)
+        v = dit_forward_varlen(W, cfg, xs, lens, torch.full((n,), ts[s], device=dev),
+                               torch.full((n,), dts[s], device=dev), g_cond, regime)
         v = v[patch_rows].reshape(n, P, -1)
         z = R.r(z + R.r(v * dts[s]))
     return z

@@ -61,3 +61,19 @@ def test_library_carries_gfx950_code_object():
             pytest.skip("objcopy unavailable")
         data = open(out, "rb").read()
     assert b"amdgcn-amd-amdhsa--gfx950" in data
+
+
+def test_paged_wrappers_take_flash_attn_positional_order():
+    """flash-attn 2.8.3's parameter lists (positional order and names), so a
+    positional call from layers/attention.py binds the same arguments."""
+    import inspect
+
+    from nanovllm_dots_amd import paged_attention as PA
+    varlen = ["q", "k", "v", "cu_seqlens_q", "cu_seqlens_k", "max_seqlen_q", "max_seqlen_k", "dropout_p",
+              "softmax_scale", "causal", "window_size", "softcap", "alibi_slopes", "deterministic",
+              "return_attn_probs", "block_table"]
+    kvcache = ["q", "k_cache", "v_cache", "k", "v", "rotary_cos", "rotary_sin", "cache_seqlens",
+               "cache_batch_idx", "cache_leftpad", "block_table", "softmax_scale", "causal", "window_size",
+               "softcap", "rotary_interleaved", "alibi_slopes", "num_splits", "return_softmax_lse"]
+    assert list(inspect.signature(PA.flash_attn_varlen_func).parameters) == varlen
+    assert list(inspect.signature(PA.flash_attn_with_kvcache).parameters) == kvcache

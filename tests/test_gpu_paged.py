@@ -79,7 +79,8 @@ def test_chunked_append_paged_matches_oracle(lq):
     print(f"append lq={lq} lk={lk}", flush=True)
     kc, vc, bt = _paged(lk, Hkv, hd, bs, seed=sum(lq))
     q = _bf(torch.randn(sum(lq), H, hd, generator=torch.Generator().manual_seed(2)))
-    out = flash_attn_varlen_func(q, kc, vc, max(lq), _cu(lq).cuda(), max(lk), _cu(lk).cuda(),
+    out = flash_attn_varlen_func(q, kc, vc, cu_seqlens_q=_cu(lq).cuda(), cu_seqlens_k=_cu(lk).cuda(),
+                                 max_seqlen_q=max(lq), max_seqlen_k=max(lk),
                                  softmax_scale=hd ** -0.5, causal=True, block_table=bt.cuda())
     ref = P.attention(q.cpu(), kc.cpu(), vc.cpu(), _cu(lq), seqlens_k=lk, block_table=bt.tolist(), block_size=bs,
                       scale=hd ** -0.5)
@@ -99,7 +100,7 @@ def test_prefill_contiguous_matches_oracle(causal):
     k = _bf(torch.randn(tot, Hkv, hd, generator=g))
     v = _bf(torch.randn(tot, Hkv, hd, generator=g))
     cu = _cu(lens)
-    out = flash_attn_varlen_func(q, k, v, max(lens), cu.cuda(), max(lens), cu.cuda(), softmax_scale=0.1,
+    out = flash_attn_varlen_func(q, k, v, cu.cuda(), cu.cuda(), max(lens), max(lens), softmax_scale=0.1,
                                  causal=causal)
     ref = P.attention(q.cpu(), k.cpu(), v.cpu(), cu, cu_k=cu, scale=0.1, causal=causal)
     _check(out, ref, f"prefill-{causal}")
@@ -158,9 +159,9 @@ def test_rejected_inputs():
     k = _bf(torch.randn(3, Hkv, hd))
     cu = _cu([3]).cuda()
     with pytest.raises(RuntimeError, match="head_dim"):
-        flash_attn_varlen_func(q, k, k, 3, cu, 3, cu, causal=True)
+        flash_attn_varlen_func(q, k, k, cu, cu, 3, 3, causal=True)
     with pytest.raises(NotImplementedError):
-        flash_attn_varlen_func(q, k, k, 3, cu, 3, cu, causal=True, window_size=(8, 0))
+        flash_attn_varlen_func(q, k, k, cu, cu, 3, 3, causal=True, window_size=(8, 0))
     # pages that are not a multiple of 256 tokens, and a short workspace
     lib = _lib.lib()
     hd = 64

@@ -1,9 +1,20 @@
-"""HIP path vs the oracle (CPU, bf16 regime) through the C ABI. GPU only.
+"""HIP path vs the oracle through the C ABI. GPU only.
 
-Tolerances: latents after the full NFE=4 solve must reach per-row cosine
->= 0.9999 and max |diff| <= 0.02 * max |ref| against the oracle; the bf16
-GEMM's float32 output must match torch's fp32 matmul of the same bf16 operands
-to 1e-5 relative (accumulation order is the only difference)."""
+Two oracle regimes, both on the same bf16-valued parameters and inputs as the
+HIP head (the reference loads its checkpoint as bf16, N/loader.py:58-63):
+
+* fp32 — the reference's CPU path, pinned bit for bit by fixtures the
+  reference's own DiT wrote (tests/golden). This is the parity bar: latents
+  after the full NFE=4 solve reach per-row cosine >= 0.9999 and
+  max |diff| <= 0.02 * max |ref|. One DiT forward's velocities (not latents)
+  reach per-row cosine >= 0.9998 and the same max |diff|: on the full-size
+  forward the bf16 restatement itself reaches only 0.99992 against fp32.
+* bf16 — the fp32 oracle with bf16 rounding where CUDA autocast rounds; the HIP
+  path tracks it more closely (same bars). Its rounding points are the
+  oracle's own reading of autocast, so no parity claim rests on it alone.
+
+The bf16 GEMM's float32 output must match torch's fp32 matmul of the same bf16
+operands to 1e-5 relative (accumulation order is the only difference)."""
 from __future__ import annotations
 
 import ctypes as C
@@ -19,6 +30,7 @@ pytestmark = pytest.mark.gpu
 
 LAT_COS = 0.9999
 LAT_MAXABS_FRAC = 0.02
+FWD_FP32_COS = 0.9998   # one forward's velocities against the fp32 oracle
 
 
 def _head(cfg, seed=0):
@@ -38,14 +50,31 @@ def _cuda_bf16(t):
     return t.to(device="cuda", dtype=torch.bfloat16).contiguous()
 
 
-def _assert_latents(got, ref, ld, label):
+def _assert_latents(got, ref, ld, label, cos_bar=LAT_COS):
     got, ref = got.float().cpu(), ref.float().cpu()
     cmin, cmean = cos_stats(got, ref, ld)
     err = (got - ref).abs().max().item()
     scale = ref.abs().max().item()
     print(f"{label}: cos min {cmin:.6f} mean {cmean:.6f} maxabs {err:.4g} (|ref| {scale:.3g})", flush=True)
-    assert cmin >= LAT_COS, f"{label}: cos min {cmin:.6f}"
+    assert cmin >= cos_bar, f"{label}: cos min {cmin:.6f}"
     assert err <= LAT_MAXABS_FRAC * scale, f"{label}: max abs {err}"
+
+
+def _fp32_solve(Wb, cfg, hist, g, noise, device="cpu"):
+    """The fp32 oracle's MeanFlow solve of the requests ``hist`` (packed rows,
+    padding-transparent, so equal to the padded solve) on ``device``."""
+    dev = torch.device(device)
+    Wd = {k: v.to(dev) for k, v in Wb.items()} if dev.type != "cpu" else Wb
+    hd = [h.float().to(dev) for h in hist]
+    gd = g.float().to(dev) if g is not None else None
+    assert not torch.backends.cuda.matmul.allow_tf32   # full float32 products
+    with torch.no_grad():
+        return R.meanflow_solve_varlen(Wd, cfg, hd, gd, noise.float().to(dev), 4, "fp32").cpu()
+
+
+def _assert_vs_fp32(got, Wb, cfg, hist, g, noise, label, device="cpu"):
+    """HIP latents vs the fixture-pinned fp32 oracle at the parity bar."""
+    _assert_latents(got, _fp32_solve(Wb, cfg, hist, g, noise, device), cfg.latent_dim, label + " vs fp32")
 
 
 # ----------------------------------------------------------------------------- GEMM
@@ -123,13 +152,17 @@ def test_dit_forward_matches_oracle(name):
     gc = R.round_bf16(torch.from_numpy(0.5 * rs.standard_normal((n, cfg.hidden)).astype(np.float32)))
     print(f"dit_forward {name} lens={lens}", flush=True)
     ref = R.dit_forward(Wb, cfg, x, t, dur, mask, pos, gc, regime="bf16")
+    ref32 = R.dit_forward(Wb, cfg, x, t, dur, mask, pos, gc, regime="fp32")
     got = HipDiT(head=head, strict=True)(x=_cuda_bf16(x), timesteps=t.cuda(), duration=dur.cuda(),
                                          attn_mask=None, pos_ids=pos.cuda(), g_cond=_cuda_bf16(gc))
     got = got.float().cpu()
     for i, L in enumerate(lens):
         rows = list(range(L)) + list(range(T - cfg.patch, T))
         cmin, _ = cos_stats(got[i, rows], ref[i, rows])
+        c32, _ = cos_stats(got[i, rows], ref32[i, rows])
+        print(f"  request {i} (c={L}): cos min {cmin:.6f} vs bf16, {c32:.6f} vs fp32", flush=True)
         assert cmin >= LAT_COS, (i, L, cmin)
+        assert c32 >= FWD_FP32_COS, (i, L, c32)
         pad = [r for r in range(T) if r not in rows]
         assert torch.all(got[i, pad] == 0)
 
@@ -146,6 +179,7 @@ def test_meanflow_solve_matches_oracle(name):
     got = mf(input_sequence=_cuda_bf16(inp), attn_mask=mask.cuda(), pos_ids=pos.cuda(),
              g_cond=_cuda_bf16(g), noise=_cuda_bf16(noise))
     _assert_latents(got, ref, cfg.latent_dim, f"meanflow-{name}")
+    _assert_vs_fp32(got, Wb, cfg, hist, g, noise, f"meanflow-{name}")
 
 
 def test_padding_transparency_bit_exact():
@@ -177,6 +211,7 @@ def test_shape_changes_without_recapture_and_shrink():
         got = mf(input_sequence=_cuda_bf16(inp), attn_mask=None, pos_ids=pos.cuda(),
                  g_cond=_cuda_bf16(g), noise=_cuda_bf16(noise))
         _assert_latents(got, ref, cfg.latent_dim, f"shape{k} n={n}")
+        _assert_vs_fp32(got, Wb, cfg, hist, g, noise, f"shape{k} n={n}")
 
 
 def test_nfe_mismatch_and_bad_layout_raise():
@@ -233,9 +268,11 @@ def test_full_size_one_step_forward_c2():
     dt = torch.full((n,), 0.25)
     print(f"c2 forward lens={lens}", flush=True)
     ref = R.dit_forward(Wb, cfg, x, t, dt, mask, pos, g, regime="bf16")[:, T - cfg.patch:]
+    ref32 = R.dit_forward(Wb, cfg, x, t, dt, mask, pos, g, regime="fp32")[:, T - cfg.patch:]
     got = HipDiT(head=head)(x=_cuda_bf16(x), timesteps=t.cuda(), duration=dt.cuda(), pos_ids=pos.cuda(),
                             g_cond=_cuda_bf16(g))[:, T - cfg.patch:]
     _assert_latents(got, ref, cfg.latent_dim, "c2-forward")
+    _assert_latents(got, ref32, cfg.latent_dim, "c2-forward vs fp32", cos_bar=FWD_FP32_COS)
 
 
 def test_full_size_nfe4_solve():
@@ -250,6 +287,7 @@ def test_full_size_nfe4_solve():
     got = mf(input_sequence=_cuda_bf16(inp), attn_mask=None, pos_ids=pos.cuda(), g_cond=_cuda_bf16(g),
              noise=_cuda_bf16(noise))
     _assert_latents(got, ref, cfg.latent_dim, "full-nfe4")
+    _assert_vs_fp32(got, Wb, cfg, hist, g, noise, "full-nfe4")
 
 
 @pytest.mark.parametrize("M,K,N,tile,epi", [(36937, 4096, 1024, 8, 4), (36937, 1024, 4096, 8, 1),

@@ -15,7 +15,7 @@ import pytest
 import torch
 
 from oracle import dit_ref as R
-from test_gpu_parity import FULL, VARIANTS, _assert_latents, _cuda_bf16, _head, _inputs
+from test_gpu_parity import FULL, VARIANTS, _assert_latents, _assert_vs_fp32, _cuda_bf16, _head, _inputs
 
 pytestmark = pytest.mark.gpu
 
@@ -48,6 +48,7 @@ def test_varlen_equals_padded_bit_exact(name):
     assert torch.equal(got, padded)
     ref = R.meanflow_solve_varlen(Wb, cfg, hist, g, noise, 4, "bf16")
     _assert_latents(got, ref, cfg.latent_dim, f"varlen-{name}")
+    _assert_vs_fp32(got, Wb, cfg, hist, g, noise, f"varlen-{name}")
 
 
 def test_varlen_mixed_strides_and_views():
@@ -112,7 +113,7 @@ def test_full_size_varlen_equals_padded():
     """12 blocks, H=1024: 8 requests with contexts U{64..512}, varlen == padded."""
     from nanovllm_dots_amd import HipMeanflow
     cfg = FULL
-    head, _ = _head(cfg, seed=2)
+    head, Wb = _head(cfg, seed=2)
     mf = HipMeanflow(None, num_steps=4, dit=object(), head=head, strict=True)
     lens, hist, noise, inp, mask, pos, g = _inputs(cfg, 8, 64, 512, seed=19)
     print(f"full varlen lens={lens}", flush=True)
@@ -121,3 +122,4 @@ def test_full_size_varlen_equals_padded():
     got = mf.solve_varlen(sequences=_engine_states(hist, extra_rows=3, seed=20), lengths=lens,
                           g_cond=_cuda_bf16(g), noise=_cuda_bf16(noise))
     assert torch.equal(got, padded)
+    _assert_vs_fp32(got, Wb, cfg, hist, g, noise, "full varlen", device="cuda")

@@ -84,13 +84,19 @@ def _small(seed=3):
 
 
 def test_bf16_regime_tracks_fp32():
-    cfg, W = _small()
-    lens, hist, noise = R.synthetic_requests(3, 5, 20, cfg, seed=2)
-    inp, mask, pos, g = R.pack_fm_inputs(hist, cfg.patch, cfg.hidden)
-    z32 = R.meanflow_solve(W, cfg, inp, mask, pos, g, noise, 4, "fp32")
-    zb = R.meanflow_solve(R.weights_for_regime(W, "bf16"), cfg, inp, mask, pos, g, noise, 4, "bf16")
+    """At full size (12 blocks, hidden 1024, MLP 4096) and on the same
+    bf16-valued parameters, the bf16 regime's latents after the NFE=4 solve stay
+    within the parity bar of the fixture-pinned fp32 regime: per-row cosine
+    >= 0.9999, max |diff| <= 0.02 * max |ref|."""
+    cfg = R.DitConfig(hidden=1024, heads=16, ffn=4096, n_blocks=12, latent_dim=64, patch=16)
+    Wb = R.weights_for_regime(R.random_dit_weights(cfg, 1), "bf16")
+    lens, hist, noise = R.synthetic_requests(2, 64, 160, cfg, seed=3)
+    z32 = R.meanflow_solve_varlen(Wb, cfg, hist, None, noise, 4, "fp32")
+    zb = R.meanflow_solve_varlen(Wb, cfg, hist, None, noise, 4, "bf16")
     cmin, _ = cos_stats(z32, zb, cfg.latent_dim)
-    assert cmin > 0.995
+    err = (zb - z32).abs().max().item()
+    assert cmin >= 0.9999, cmin
+    assert err <= 0.02 * z32.abs().max().item(), err
     # bf16 regime values are bf16-representable
     assert torch.equal(zb, R.round_bf16(zb))
 
