@@ -24,6 +24,13 @@ __device__ __forceinline__ void wait_vm_lgkm0() {
   __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (0 << 8) | ((N >> 4) << 14));
 }
 
+// s_waitcnt vmcnt(n) only (lgkmcnt and expcnt at their maxima: not waited for)
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
 // float32 multiply / add that the compiler may not fuse into an FMA: sequences
 // that reproduce torch's separately rounded elementwise ops use these.
 __device__ __forceinline__ float mul_rn(float a, float b) {

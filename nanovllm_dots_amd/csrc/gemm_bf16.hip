@@ -35,6 +35,17 @@ namespace {
 //           1 KB DMA instruction, so a step's 64 instructions queue for ~1000
 //           cycles and hold up the MFMAs of every wave that issued one; the half
 //           that issues none starts its MFMAs right after the barrier.
+//  SCHED 2: one wave per SIMD (4 waves, 128x128 per wave, accumulators in
+//           AGPRs), BK 32 in 5 stages with the DMA 4 steps ahead. Each wave
+//           spreads its DMA over its MFMAs, one 1 KB instruction after every 4
+//           MFMAs: the vector-memory path (64 B per cycle per CU) absorbs the
+//           CU's 4 instructions per 128 cycles as they come, so its queue never
+//           fills and no wave stalls behind it. One barrier per step, between its
+//           two 16-deep slices. The epilogue stages rows in the stage the next
+//           tile's prologue leaves free. It needs a third fewer LDS fragment reads
+//           per MFMA than SCHED 1; under random bf16 operands both run into the
+//           chip's power limit at about the same rate, and SCHED 1 has the
+//           smaller per-tile overhead, so production shapes use SCHED 1.
 template <int BM_, int BN_, int BK_, int ST_, int WM_, int WN_, int SCHED_ = 0>
 struct Cfg {
   static constexpr int BM = BM_, BN = BN_, BK = BK_, ST = ST_, WM = WM_, WN = WN_, SCHED = SCHED_;
@@ -51,6 +62,8 @@ struct Cfg {
   static constexpr int RPR = DW * ROWS_PER_DMA;     // rows per DMA round of the workgroup
   static constexpr int AJ = BM / RPR, BJ = BN / RPR;
   static constexpr int LPS = AJ + BJ;               // DMA instructions per wave per K step
+  // K pieces per leftover tile at most (its last piece reads the others' partial sums)
+  static constexpr int MAX_SPLIT = SCHED == 2 ? 2 : 64;
   static constexpr int LDS_BYTES = ST * (BM + BN) * BK * 2;
   // two workgroups per CU when both fit in LDS (then <= 256 registers per lane)
   static constexpr int WG_PER_CU = (NW <= 4 && 2 * LDS_BYTES <= 160 * 1024) ? 2 : 1;
@@ -58,8 +71,10 @@ struct Cfg {
   static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tile");
   static_assert(BM % RPR == 0 && BN % RPR == 0, "DMA rounds");
   static_assert(BK == 32 || BK == 64, "BK");
-  static_assert(ST >= 1 && ST <= 4, "stages");
+  static_assert(ST >= 1 && ST <= (SCHED == 2 ? 5 : 4), "stages");
   static_assert(!HD || NW == 8, "half DMA: 8 waves");
+  static_assert(SCHED != 2 || (NW == 4 && ST == 5 && BK == 32 && AJ == 4 && BJ == 4 && RM * RN == 16),
+                "SCHED 2: 4 waves, 128x128 per wave, BK 32 x 5 stages");
 };
 
 // LDS tile layout: rows of BK bf16 (BK/8 16-B chunks), row-major, logical chunk
@@ -71,6 +86,15 @@ struct Cfg {
 constexpr int kBufferFlags = 0x00020000;
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// f(integral_constant<int, I>) for I = 0 .. N-1, unrolled at compile time
+template <int N, int I = 0, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (I < N) {
+    f(std::integral_constant<int, I>{});
+    static_for<N, I + 1>(f);
+  }
+}
 
 template <int CH>
 __device__ __forceinline__ int swz(int row) {
@@ -506,13 +530,15 @@ constexpr int kMinSplitSteps = 4;
 // leftover tile; at a fixed place for every tile shape, zero between calls),
 // then one BM x BN float32 partial tile per workgroup
 constexpr long kSplitCounters = 4096;
-__device__ __forceinline__ void split_plan(int chunk_x, int per_xcd, int KT, int& full_x, int& split) {
+__device__ __forceinline__ void split_plan(int chunk_x, int per_xcd, int KT, int max_split, int& full_x,
+                                           int& split) {
   full_x = chunk_x;
   split = 1;
   const int rounds = chunk_x / per_xcd, tail = chunk_x - rounds * per_xcd;
   if (tail == 0) return;
   int sp = per_xcd / tail;
   if (sp > KT / kMinSplitSteps) sp = KT / kMinSplitSteps;
+  if (sp > max_split) sp = max_split;
   if (sp < 2) return;
   full_x = rounds * per_xcd;
   split = sp;
@@ -528,20 +554,25 @@ gemm_mfma_kernel(GemmArgs a) {
   __shared__ __attribute__((aligned(1024))) uint16_t sA1[ST > 1 ? BM * BK : 8], sB1[ST > 1 ? BN * BK : 8];
   __shared__ __attribute__((aligned(1024))) uint16_t sA2[ST > 2 ? BM * BK : 8], sB2[ST > 2 ? BN * BK : 8];
   __shared__ __attribute__((aligned(1024))) uint16_t sA3[ST > 3 ? BM * BK : 8], sB3[ST > 3 ? BN * BK : 8];
-  __shared__ int s_flag;  // K-split: this workgroup completed its tile
+  __shared__ __attribute__((aligned(1024))) uint16_t sA4[ST > 4 ? BM * BK : 8], sB4[ST > 4 ? BN * BK : 8];
+  // K-split: this workgroup completed its tile. Kept in stage 0, which no DMA
+  // fills and no epilogue stages into while the flag is in use.
+  int& s_flag = *reinterpret_cast<int*>(sA0);
   auto stA = [&](auto stc) -> uint16_t* {
     constexpr int s = decltype(stc)::value;
     if constexpr (s == 0) return sA0;
     else if constexpr (s == 1) return sA1;
     else if constexpr (s == 2) return sA2;
-    else return sA3;
+    else if constexpr (s == 3) return sA3;
+    else return sA4;
   };
   auto stB = [&](auto stc) -> uint16_t* {
     constexpr int s = decltype(stc)::value;
     if constexpr (s == 0) return sB0;
     else if constexpr (s == 1) return sB1;
     else if constexpr (s == 2) return sB2;
-    else return sB3;
+    else if constexpr (s == 3) return sB3;
+    else return sB4;
   };
 
   const int M = a.M_dev ? *a.M_dev : a.M;
@@ -568,7 +599,7 @@ gemm_mfma_kernel(GemmArgs a) {
   int chunk_x = total - xcd * chunk;
   chunk_x = chunk_x < 0 ? 0 : (chunk_x > chunk ? chunk : chunk_x);
   int full_x = chunk_x, split = 1;
-  if (a.ws != nullptr) split_plan(chunk_x, per_xcd, K / BK, full_x, split);
+  if (a.ws != nullptr) split_plan(chunk_x, per_xcd, K / BK, C::MAX_SPLIT, full_x, split);
   auto tile_at = [&](int jt) { return jt < full_x ? xcd * chunk + jt : -1; };
   // Grouped order: the per_xcd tiles an XCD runs at once cover GM row blocks x
   // per_xcd/GM column blocks (row block fastest), so each A row block and W
@@ -716,6 +747,152 @@ gemm_mfma_kernel(GemmArgs a) {
     if constexpr (ST > 2) { if (1 < KTi) dma(std::integral_constant<int, 1 % ST>{}, kb + 1); }
     if constexpr (ST > 3) { if (2 < KTi) dma(std::integral_constant<int, 2 % ST>{}, kb + 2); }
   };
+  // ---- SCHED 2: one wave per SIMD, DMA spread over the MFMAs ----
+  // DMA(j) = the A rows of K step j (4 instructions per wave, issued in slice 1
+  // of step j - D2) and its B rows (4, in slice 0 of step j - D2 + 1): ST - 1
+  // steps ahead, into stage j % ST.
+  constexpr int D2 = C::SCHED == 2 ? ST - 1 : 3;  // (other schedules never run this code)
+  // vector-memory ops a staged epilogue issues after the next tile's prologue
+  // (stores, residual / gate loads) plus the row -> request loads of the next
+  // tile's start; -1: unknown or too many to count (then those waits drain fully)
+  constexpr int kVm2Raw = (EPI == EPI_QKV || !Staged<C, EPI>::value)
+                              ? -1
+                              : Staged<C, EPI>::kVmAfter + (Staged<C, EPI>::kRes ? C::RM * Staged<C, EPI>::JB : 0);
+  constexpr int kVm2 = kVm2Raw > 63 ? 63 : kVm2Raw;
+  constexpr auto epi_n = [](int base) constexpr { return kVm2 < 0 ? 0 : (base + kVm2 > 63 ? 63 : base + kVm2); };
+  constexpr int kSteady2 = 8 * (D2 - 2);   // mid-step: DMA(k+2 .. k+D2-1) issued after DMA(k+1)
+  constexpr int kStart2 = kSteady2 + 4;    // tile start: DMA(1 .. D2-2) and the A rows of DMA(D2-1)
+  bf16x8 g_a[2][C::RM], g_b[2][C::RN];  // fragments of the two 16-deep slices of a step
+  // DMA instruction d (0..3) of half h (0: A rows, 1: B rows) of K step ks into stage stc
+  auto dma1 = [&](auto stc, int ks, int h, int d) __attribute__((always_inline)) {
+    const int koff = ks * BK * 2;
+    if (h == 0) {
+      uint32_t vo = va + (uint32_t)d * a_round;
+      asm volatile("" : "+v"(vo));
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          ra, DFH_LPTR(stA(stc) + (d * C::RPR + dma_wave * C::ROWS_PER_DMA) * BK), 16, vo, koff, 0, 0);
+    } else {
+      uint32_t vo = vb + (uint32_t)d * b_round;
+      asm volatile("" : "+v"(vo));
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rb, DFH_LPTR(stB(stc) + (d * C::RPR + dma_wave * C::ROWS_PER_DMA) * BK), 16, vo, koff, 0, 0);
+    }
+  };
+  // fragment read r (0..7) of slice `half` of the step in stage stc, in the order
+  // the slice's MFMAs first use them: b0, a0, a1, a2, a3, b1, b2, b3
+  auto frag1 = [&](auto stc, int half, int r, bf16x8 (&fa)[C::RM], bf16x8 (&fb)[C::RN])
+      __attribute__((always_inline)) {
+    const int ch = 2 * half + hi;
+    if (r == 0) {
+      fb[0] = *reinterpret_cast<const bf16x8*>(stB(stc) + lds_off<CH>(fb_row, ch));
+    } else if (r <= C::RM) {
+      fa[r - 1] = *reinterpret_cast<const bf16x8*>(stA(stc) + lds_off<CH>(fa_row + (r - 1) * 32, ch));
+    } else {
+      fb[r - C::RM] = *reinterpret_cast<const bf16x8*>(stB(stc) + lds_off<CH>(fb_row + (r - C::RM) * 32, ch));
+    }
+  };
+  // one 16-deep slice: MFMA t on (fb[t / RM], fa[t % RM]); after MFMA 2j+1 the
+  // next slice's fragment read j, after MFMA 4j+2 the DMA instruction j.
+  // Z: the tile's first slice, accumulating onto zero.
+  auto slice2 = [&](auto zc, bf16x8 (&fa)[C::RM], bf16x8 (&fb)[C::RN], auto&& rd, auto&& dm)
+      __attribute__((always_inline)) {
+    constexpr bool Z = decltype(zc)::value;
+#pragma unroll
+    for (int t = 0; t < 16; ++t) {
+      auto& c = acc[t / C::RM][t % C::RM];
+      if constexpr (Z) c = Op::mma(fb[t / C::RM], fa[t % C::RM], typename Op::acc_t{});
+      else c = Op::mma(fb[t / C::RM], fa[t % C::RM], c);
+      __builtin_amdgcn_sched_barrier(0);
+      if (t & 1) {
+        rd(t >> 1);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      if ((t & 3) == 2) {
+        dm(t >> 2);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+  };
+  // mid-step wait of a guarded step: nb = DMA steps issued after DMA(k+1) (0 .. D2-2);
+  // epi: the epilogue's memory ops were also issued after it
+  auto mid_wait = [&](int nb, bool epi) __attribute__((always_inline)) {
+    if (nb >= 2) { if (epi) wait_vm<epi_n(16)>(); else wait_vm<16>(); }
+    else if (nb == 1) { if (epi) wait_vm<epi_n(8)>(); else wait_vm<8>(); }
+    else { if (epi) wait_vm<epi_n(0)>(); else wait_vm<0>(); }
+  };
+  // K step k in stage s (= k % ST). Slice 0: MFMAs on g[0], reads of this
+  // step's slice 1 into g[1], the B rows of DMA(k+D2-1). Mid-step: this wave's
+  // DMA(k+1) has landed (vmcnt), then the barrier makes every wave's visible.
+  // Slice 1: MFMAs on g[1], reads of step k+1's slice 0 into g[0], the A rows of
+  // DMA(k+D2). Stage (k+D2-1) % ST last held step k-2 and stage (k+D2) % ST step
+  // k-1: every wave finished reading them before the barrier of step k-1, resp. k.
+  // G: guard the reads / DMA past the last step; epi: see mid_wait; Z: first step.
+  auto step2 = [&](auto stc, auto gc, auto zc, int k, bool epi) __attribute__((always_inline)) {
+    constexpr int s = decltype(stc)::value;
+    constexpr bool G = decltype(gc)::value;
+    using Sn = std::integral_constant<int, (s + 1) % ST>;
+    using Sa = std::integral_constant<int, (s + D2 - 1) % ST>;
+    using Sb = std::integral_constant<int, (s + D2) % ST>;
+    if (G && k >= KTi) return;  // uniform
+    const bool db = !G || k + D2 - 1 < KTi, rn = !G || k + 1 < KTi, da = !G || k + D2 < KTi;
+    slice2(zc, g_a[0], g_b[0], [&](int r) { frag1(stc, 1, r, g_a[1], g_b[1]); },
+           [&](int d) { if (db) dma1(Sa{}, kb + k + D2 - 1, 1, d); });
+    if constexpr (G) {
+      const int nb = KTi - k - 2;
+      mid_wait(nb < 0 ? 0 : (nb > D2 - 2 ? D2 - 2 : nb), epi);
+    } else {
+      wait_vm<kSteady2>();
+    }
+    __builtin_amdgcn_s_barrier();
+    slice2(std::false_type{}, g_a[1], g_b[1], [&](int r) { if (rn) frag1(Sn{}, 0, r, g_a[0], g_b[0]); },
+           [&](int d) { if (da) dma1(Sb{}, kb + k + D2, 0, d); });
+  };
+  // DMA(0 .. D2-2) and the A rows of DMA(D2-1)
+  auto prologue2 = [&]() __attribute__((always_inline)) {
+    static_for<D2 - 1>([&](auto j) {
+      constexpr int J = decltype(j)::value;
+      if (J < KTi) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+          for (int d = 0; d < 4; ++d) dma1(j, kb + J, h, d);
+      }
+    });
+    if (D2 - 1 < KTi) {
+#pragma unroll
+      for (int d = 0; d < 4; ++d) dma1(std::integral_constant<int, D2 - 1>{}, kb + D2 - 1, 0, d);
+    }
+  };
+  // the K loop of one item; after_epi: a staged epilogue's memory ops were issued
+  // after this item's prologue. Steps 0 .. D2-3 wait for those too; they and the
+  // last steps run guarded, the rest in unrolled groups of ST steps.
+  auto kloop2 = [&](bool after_epi) __attribute__((always_inline)) {
+    using T = std::true_type;
+    using F = std::false_type;
+    constexpr int P = D2 - 2 > 1 ? D2 - 2 : 1;  // peeled steps
+    if (KTi < D2) wait_vm<0>();
+    else if (after_epi) wait_vm<epi_n(kStart2)>();
+    else wait_vm<kStart2>();
+    __builtin_amdgcn_s_barrier();
+#pragma unroll
+    for (int r = 0; r < 8; ++r) frag1(std::integral_constant<int, 0>{}, 0, r, g_a[0], g_b[0]);
+    step2(std::integral_constant<int, 0>{}, T{}, T{}, 0, after_epi);
+    static_for<P - 1>([&](auto j) {
+      constexpr int J = decltype(j)::value + 1;
+      step2(std::integral_constant<int, J % ST>{}, T{}, F{}, J, after_epi && J <= D2 - 3);
+    });
+    int k = P;
+    for (; k + ST - 1 + D2 < KTi; k += ST)
+      static_for<ST>([&](auto j) {
+        constexpr int J = decltype(j)::value;
+        step2(std::integral_constant<int, (P + J) % ST>{}, F{}, F{}, k + J, false);
+      });
+    for (; k < KTi; k += ST)
+      static_for<ST>([&](auto j) {
+        constexpr int J = decltype(j)::value;
+        step2(std::integral_constant<int, (P + J) % ST>{}, T{}, F{}, k + J, false);
+      });
+  };
   // the K piece of a leftover tile this workgroup runs last (piece < 0: none)
   const int tail_tiles = chunk_x - full_x;
   const int piece = (split > 1 && slot < tail_tiles * split) ? slot : -1;
@@ -731,9 +908,14 @@ gemm_mfma_kernel(GemmArgs a) {
   int tile = tile_at(jt);
   if (tile >= 0) {
     set_offsets(tile);
-    prologue();
-    wait_vm_lgkm0<0>();  // the first tile has no epilogue stores in flight
+    if constexpr (C::SCHED == 2) {
+      prologue2();
+    } else {
+      prologue();
+      wait_vm_lgkm0<0>();  // the first tile has no epilogue stores in flight
+    }
   }
+  bool after_epi = false;
   while (tile >= 0) {
     int m0, n0;
     tile_mn(tile, m0, n0);
@@ -745,7 +927,8 @@ gemm_mfma_kernel(GemmArgs a) {
         for (int t = 0; t < 16; ++t) acc[i][k][t] = 0;
     ResRows<C, EPI> rrows;
     res_rows_load<C, EPI>(a, rrows, m0, M, wm, lane);  // lands during the K loop
-    kloop();
+    if constexpr (C::SCHED == 2) kloop2(after_epi);
+    else kloop();
     // every wave is done with every stage before it is refilled
     wait_vm_lgkm0<0>();
     __builtin_amdgcn_s_barrier();
@@ -756,7 +939,8 @@ gemm_mfma_kernel(GemmArgs a) {
     const int next = tile_at(jt);
     if (next >= 0) {
       set_offsets(next);
-      prologue();
+      if constexpr (C::SCHED == 2) prologue2();
+      else prologue();
     }
     if constexpr (Staged<C, EPI>::value) {
       // the stage the prologue does not fill (ST - 1); waves split over its A and B buffers
@@ -768,6 +952,7 @@ gemm_mfma_kernel(GemmArgs a) {
     } else {
       run_epilogue<C, EPI>(a, acc, m0, n0, M, wm, wn, l32, hi);
     }
+    after_epi = true;
     tile = next;
   }
   if (piece < 0) return;
@@ -780,15 +965,20 @@ gemm_mfma_kernel(GemmArgs a) {
   const int tt = piece / split;  // leftover tile within the XCD
   const int tile_p = set_item(piece, true);
   set_offsets(tile_p);
-  prologue();
-  wait_vm_lgkm0<0>();
+  if constexpr (C::SCHED == 2) {
+    prologue2();
+  } else {
+    prologue();
+    wait_vm_lgkm0<0>();
+  }
 #pragma unroll
   for (int i = 0; i < C::RN; ++i)
 #pragma unroll
     for (int k = 0; k < C::RM; ++k)
 #pragma unroll
       for (int t = 0; t < 16; ++t) acc[i][k][t] = 0;
-  kloop();
+  if constexpr (C::SCHED == 2) kloop2(false);
+  else kloop();
   using E = typename Op::elem_t;
   auto part_off = [&](int i, int k, int q) {
     return (((((long)wave * C::RN + i) * C::RM + k) * 4 + q) * 64 + lane) * 4;
@@ -931,12 +1121,13 @@ using T5 = Cfg<128, 256, 32, 3, 2, 2>;  // 4 waves, 64x128 per wave, 72 KB: two 
 using T6 = Cfg<256, 128, 64, 3, 2, 2>;  // 4 waves, 3 stages, 144 KB
 using T7 = Cfg<128, 128, 32, 4, 2, 2>;  // 4 waves, 4 stages of BK 32, 64 KB: two per CU
 using T8 = Cfg<256, 256, 64, 2, 2, 4, 1>;  // T0 with the DMA of a step issued by one half
-constexpr int kNumTiles = 9;
-const int kTileBM[kNumTiles] = {T0::BM, T1::BM, T2::BM, T3::BM, T4::BM, T5::BM, T6::BM, T7::BM, T8::BM};
-const int kTileBN[kNumTiles] = {T0::BN, T1::BN, T2::BN, T3::BN, T4::BN, T5::BN, T6::BN, T7::BN, T8::BN};
-const int kTileBK[kNumTiles] = {T0::BK, T1::BK, T2::BK, T3::BK, T4::BK, T5::BK, T6::BK, T7::BK, T8::BK};
+using T9 = Cfg<256, 256, 32, 5, 2, 2, 2>;  // 4 waves, 128x128 per wave (AGPRs), DMA spread over the MFMAs, 160 KB
+constexpr int kNumTiles = 10;
+const int kTileBM[kNumTiles] = {T0::BM, T1::BM, T2::BM, T3::BM, T4::BM, T5::BM, T6::BM, T7::BM, T8::BM, T9::BM};
+const int kTileBN[kNumTiles] = {T0::BN, T1::BN, T2::BN, T3::BN, T4::BN, T5::BN, T6::BN, T7::BN, T8::BN, T9::BN};
+const int kTileBK[kNumTiles] = {T0::BK, T1::BK, T2::BK, T3::BK, T4::BK, T5::BK, T6::BK, T7::BK, T8::BK, T9::BK};
 const int kTileWTN[kNumTiles] = {T0::WTN, T1::WTN, T2::WTN, T3::WTN, T4::WTN, T5::WTN, T6::WTN, T7::WTN,
-                                 T8::WTN};
+                                 T8::WTN, T9::WTN};
 
 template <class Op, int EPI>
 hipError_t dispatch_tiles(const GemmArgs& a, hipStream_t s, int tile) {
@@ -950,6 +1141,7 @@ hipError_t dispatch_tiles(const GemmArgs& a, hipStream_t s, int tile) {
     case 6: return launch<T6, Op, EPI>(a, s);
     case 7: return launch<T7, Op, EPI>(a, s);
     case 8: return launch<T8, Op, EPI>(a, s);
+    case 9: return launch<T9, Op, EPI>(a, s);
     default: return hipErrorInvalidValue;
   }
 }

@@ -83,7 +83,11 @@ GEMM_CASES = [(1, 64, 64, 3), (37, 128, 256, 2), (300, 1024, 1024, -1), (700, 10
               (777, 512, 1024, 4), (1500, 4096, 1024, 0), (20, 256, 64, 0), (333, 256, 192, 1),
               (1111, 1024, 1024, 5), (600, 1024, 4096, 6), (259, 512, 1024, 7), (1234, 3072, 1024, 1),
               (100, 512, 96, 7), (70, 256, 160, 5), (1500, 4096, 1024, 8), (3001, 1024, 4096, 8),
-              (20, 256, 64, 8)]
+              (20, 256, 64, 8),
+              # tile 9 (4 waves, AGPR accumulators, BK 32 x 5 stages): K steps 1, 2, 3, 4, 5 exercise the
+              # guarded prologue / tail paths, the larger ones the unrolled steady state
+              (1500, 4096, 1024, 9), (3001, 1024, 4096, 9), (700, 512, 32, 9), (333, 256, 64, 9),
+              (37, 256, 96, 9), (300, 768, 128, 9), (513, 256, 160, 9), (2000, 1024, 2048, 9)]
 
 
 @pytest.mark.parametrize("M,N,K,tile", GEMM_CASES)
@@ -104,18 +108,19 @@ def test_gemm_f32_out_matches_torch(M, N, K, tile):
     assert rel < 1e-5, rel
 
 
+@pytest.mark.parametrize("tile", [-1, 9])
 @pytest.mark.parametrize("epi", [0, 1])
-def test_gemm_bf16_epilogues(epi):
+def test_gemm_bf16_epilogues(epi, tile):
     from nanovllm_dots_amd import _lib
     lib = _lib.lib()
-    M, N, K = 333, 512, 1024
+    M, N, K = 333 if tile < 0 else 3333, 512, 1024
     g = torch.Generator(device="cpu").manual_seed(epi)
     A = torch.randn(M, K, generator=g).bfloat16().cuda()
     B = (0.03 * torch.randn(N, K, generator=g)).bfloat16().cuda()
     bias = (0.1 * torch.randn(N, generator=g)).bfloat16().cuda()
     out = torch.empty(M, N, device="cuda", dtype=torch.bfloat16)
     _lib.check(lib.dfh_gemm_bf16(_lib.ptr(A), K, _lib.ptr(B), K, _lib.ptr(out), N, _lib.ptr(bias),
-                                 M, N, K, epi, -1, _lib.stream_ptr()))
+                                 M, N, K, epi, tile, _lib.stream_ptr()))
     pre = (A.float() @ B.float().t() + bias.float()).bfloat16().float()
     ref = pre
     if epi == 1:
