@@ -264,8 +264,11 @@ typedef struct DfhPagedAttnArgs {
   long out_stride;
   float softmax_scale;
   int causal;
-  void* workspace;
+  void* workspace;                  /* 256-B aligned */
   long workspace_bytes;
+  long total_q;                     /* query rows of the batch (q's first dimension), or 0 if unknown:
+                                       bounds the row tiles, so the workspace is sized by the batch's
+                                       actual rows instead of batch * max_seqlen_q */
 } DfhPagedAttnArgs;
 long dfh_paged_attention_workspace(const DfhPagedAttnArgs* a);
 int dfh_paged_attention(const DfhPagedAttnArgs* a, void* stream);

@@ -63,7 +63,7 @@ class DfhPagedAttnArgs(C.Structure):
         ("cu_seqlens_k", vp), ("seqlens_k", vp), ("block_table", vp),
         ("block_table_stride", C.c_int), ("block_size", C.c_int),
         ("out", vp), ("out_stride", C.c_long), ("softmax_scale", C.c_float), ("causal", C.c_int),
-        ("workspace", vp), ("workspace_bytes", C.c_long),
+        ("workspace", vp), ("workspace_bytes", C.c_long), ("total_q", C.c_long),
     ]
 
 

@@ -865,8 +865,8 @@ long dfh_paged_attention_workspace(const DfhPagedAttnArgs* a) {
   if (!a || a->batch <= 0 || a->num_kv_heads <= 0 || a->num_heads % a->num_kv_heads || a->max_seqlen_q <= 0 ||
       a->max_seqlen_k <= 0)
     return 0;
-  return 4 * dfh::paged_attention_ws_floats(a->batch, a->num_kv_heads, a->num_heads / a->num_kv_heads,
-                                            a->max_seqlen_q, a->max_seqlen_k, a->head_dim);
+  return dfh::paged_attention_ws_bytes(a->batch, a->num_kv_heads, a->num_heads / a->num_kv_heads, a->max_seqlen_q,
+                                      a->max_seqlen_k, a->head_dim, a->total_q > 0 ? a->total_q : 0);
 }
 
 int dfh_paged_attention(const DfhPagedAttnArgs* a, void* stream) {
@@ -890,6 +890,7 @@ int dfh_paged_attention(const DfhPagedAttnArgs* a, void* stream) {
     return fail("dfh_paged_attention: bad strides");
   if (((uintptr_t)a->q | (uintptr_t)a->k | (uintptr_t)a->v) & 15)
     return fail("dfh_paged_attention: q, k, v must be 16-byte aligned");
+  if ((uintptr_t)a->workspace & 15) return fail("dfh_paged_attention: workspace must be 16-byte aligned");
   const long need = dfh_paged_attention_workspace(a);
   if (a->workspace_bytes < need)
     return fail("dfh_paged_attention: workspace %ld bytes < %ld needed", a->workspace_bytes, need);
@@ -902,7 +903,8 @@ int dfh_paged_attention(const DfhPagedAttnArgs* a, void* stream) {
   x.block_table = a->block_table; x.bt_stride = a->block_table_stride; x.block_size = a->block_size;
   x.out = static_cast<uint16_t*>(a->out); x.out_stride = a->out_stride;
   x.scale = a->softmax_scale; x.causal = a->causal;
-  x.ws = static_cast<float*>(a->workspace);
+  x.ws = a->workspace;
+  x.total_q = a->total_q > 0 ? a->total_q : 0;
   DFH_CHECK(dfh::paged_attention(x, reinterpret_cast<hipStream_t>(stream)));
   return 0;
 }

@@ -130,6 +130,7 @@ hipError_t decode_attention(const uint16_t* qk, long ldqk, const uint16_t* vt, l
 // causal, GQA). head_dim 64 or 128; block_size a multiple of 256 when paged.
 struct PagedAttnArgs {
   int batch, heads, kv_heads, head_dim, max_q, max_k;
+  long total_q;                  // query rows of the batch (0: unknown, bounded by batch * max_q)
   const uint16_t* q;
   long q_stride;                 // elements between query tokens
   const int* cu_q;               // [batch + 1]
@@ -144,9 +145,9 @@ struct PagedAttnArgs {
   long out_stride;
   float scale;
   int causal;
-  float* ws;                     // paged_attention_ws_floats(...) floats
+  void* ws;                      // paged_attention_ws_bytes(...) bytes, 256-B aligned
 };
-long paged_attention_ws_floats(int batch, int kv_heads, int group, int max_q, int max_k, int head_dim);
+long paged_attention_ws_bytes(int batch, int kv_heads, int group, int max_q, int max_k, int head_dim, long total_q);
 hipError_t paged_attention(const PagedAttnArgs& a, hipStream_t s);
 // key / value [n, D] rows (strides in elements) -> cache rows slots[i] ([num_slots, D]); slot < 0 skips
 hipError_t store_kvcache(const uint16_t* key, long key_stride, const uint16_t* value, long value_stride,

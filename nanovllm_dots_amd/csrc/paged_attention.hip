@@ -18,8 +18,14 @@
 // head h / G, G = heads / kv_heads.
 //
 // Work split (split-KV): one workgroup = one wave = 32 query rows of one
-// (sequence, KV head) against one chunk of 256 keys (wider past 32 K keys, so
-// a row has at most 128 chunks). A row is a (token, head within the group)
+// (sequence, KV head) against one chunk of keys. The (sequence, row tile) items
+// are a compact list that a one-workgroup plan kernel writes from cu_seqlens_q
+// (at most ceil(total_q * G / 32) + batch of them, so a batch of one long and
+// many short prompts is not padded to the longest). The chunk count is chosen to
+// fill the GPU with about kTargetWaves workgroups: 256-key chunks for a decode
+// of a few dozen sequences, one chunk per row tile once the tiles alone fill it
+// (then the kernel writes normalised bf16 rows itself and there is no workspace
+// of partial sums and no combine launch). A row is a (token, head within the group)
 // pair, so at decode one wave serves the G heads that share the KV head, and
 // K / V are read once for all of them. Inside the chunk the wave walks four
 // 64-key tiles with an online softmax, both products on MFMA:
@@ -29,8 +35,8 @@
 //   within each 16-key step, the same way for both operands) and V^T staged in
 //   LDS: each lane loads its columns of every V row (coalesced row reads) and
 //   writes them transposed, 4 keys per 8-B store.
-// Each chunk writes (max, sum, O) per row to the workspace; a combine kernel
-// merges the chunks of a row and writes bf16. Pages are multiples of 256
+// With several chunks, each writes (max, sum, O) per row to the workspace and a
+// combine kernel merges the chunks of a row and writes bf16. Pages are multiples of 256
 // tokens, so a 64-key tile never straddles a page.
 #include <type_traits>
 
@@ -46,6 +52,7 @@ constexpr int kMaxChunks = 128;  // chunks per row at most (the chunk widens pas
 constexpr int PT = 64;    // keys per tile
 constexpr int PR = 32;    // query rows per workgroup
 constexpr int kCombineSplit = 4;  // column slices of head_dim per combine row tile
+constexpr long kTargetWaves = 4096;  // attention workgroups (one wave each) that fill the GPU
 
 struct PagedParams {
   const uint16_t* q;
@@ -60,8 +67,9 @@ struct PagedParams {
   int bt_stride, block_size;
   uint16_t* out;
   long out_stride;
-  float* ws;
-  int kv_heads, group, n_tiles, n_chunks, chunk;  // chunk: keys per workgroup (multiple of PCH)
+  float* ws;                      // partial sums (n_chunks > 1)
+  const int2* items;             // (sequence, row tile) per item; sequence -1: no work
+  int kv_heads, group, n_chunks, chunk;  // chunk: keys per workgroup (multiple of PCH)
   float scale_log2;
   int causal;
 };
@@ -94,16 +102,19 @@ __global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) pa
   __shared__ __align__(16) float As[PR];
   const int lane = threadIdx.x, l32 = lane & 31, hi = lane >> 5;
   const int c = blockIdx.x % a.n_chunks;
-  const int it = blockIdx.x / a.n_chunks;  // sequence * n_tiles + row tile
-  const int i = it / a.n_tiles, tile = it % a.n_tiles;
+  const int it = blockIdx.x / a.n_chunks;  // item
+  const int2 item = a.items[it];
+  if (item.x < 0) return;
+  const int i = item.x, tile = item.y;
   const int g = blockIdx.y;
   const int q0 = a.cu_q[i];
   const int Lq = a.cu_q[i + 1] - q0;
   const int Lk = seq_lk(a, i);
   const int G = a.group;
   const int R = min(PR, Lq * G - tile * PR);  // rows of this tile (uniform)
-  if (R <= 0 || c * a.chunk >= Lk) return;
-  float* part = a.ws + ((long)(it * a.kv_heads + g) * a.n_chunks + c) * part_floats<HD>();
+  const bool direct = a.n_chunks == 1;       // no partial sums: normalise and write bf16 here
+  if (R <= 0 || (!direct && c * a.chunk >= Lk)) return;
+  float* part = direct ? nullptr : a.ws + ((long)(it * a.kv_heads + g) * a.n_chunks + c) * part_floats<HD>();
   // this lane's row (clamped to the last real row) and its visible-key limit
   const int r_me = min(l32, R - 1);
   const int gr = tile * PR + r_me;
@@ -113,7 +124,7 @@ __global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) pa
   const int j_max = (tile * PR + R - 1) / G;
   const int lim_max = a.causal ? min(Lk, Lk - Lq + j_max + 1) : Lk;
   const int k0 = c * a.chunk;
-  if (k0 >= lim_max) {
+  if (!direct && k0 >= lim_max) {
     if (hi == 0 && l32 < R) {
       part[l32] = -INFINITY;
       part[PR + l32] = 0.f;
@@ -235,6 +246,22 @@ __global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) pa
     }
     __syncthreads();  // Vt / As are rewritten by the next tile
   }
+  if (direct) {
+    // O / l of row r = 8*(e/4) + 4*hi + e%4 (a row that sees no key is 0)
+    if (hi == 0) As[l32] = l_run > 0.f ? 1.f / l_run : 0.f;
+    __syncthreads();
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const int r = 8 * (e >> 2) + 4 * hi + (e & 3);
+      if (r >= R) continue;
+      const float inv = As[r];
+      const int grr = tile * PR + r;
+      uint16_t* op = a.out + (long)(q0 + grr / G) * a.out_stride + (long)(g * G + grr % G) * HD + l32;
+#pragma unroll
+      for (int db = 0; db < HD / 32; ++db) op[db * 32] = f2bf(o[db][e] * inv);
+    }
+    return;
+  }
   if (hi == 0 && l32 < R) {
     part[l32] = m_run;
     part[PR + l32] = l_run;
@@ -262,7 +289,9 @@ __global__ void __launch_bounds__(256) paged_combine_kernel(PagedParams a) {
   __shared__ float Ms[PR][kMaxChunks + 1];  // chunk maxima, then weights
   __shared__ float Ls[PR][kMaxChunks + 1];
   const int it = blockIdx.x, g = blockIdx.y;
-  const int i = it / a.n_tiles, tile = it % a.n_tiles;
+  const int2 item = a.items[it];
+  if (item.x < 0) return;
+  const int i = item.x, tile = item.y;
   const int q0 = a.cu_q[i];
   const int Lq = a.cu_q[i + 1] - q0;
   const int Lk = seq_lk(a, i);
@@ -309,6 +338,37 @@ __global__ void __launch_bounds__(256) paged_combine_kernel(PagedParams a) {
   }
 }
 
+// The (sequence, row tile) items of a batch: sequence i has ceil(Lq_i * G / 32)
+// row tiles; items past the batch's total (the list is sized by a host bound)
+// are marked with sequence -1. One workgroup; a running offset carries the scan
+// of per-sequence tile counts from one block of 256 sequences to the next.
+__global__ void __launch_bounds__(256) paged_plan_kernel(const int* __restrict__ cu_q, int batch, int group,
+                                                          int n_items, int2* __restrict__ items) {
+  __shared__ int scan[256];
+  __shared__ int carry;
+  const int tid = threadIdx.x;
+  if (tid == 0) carry = 0;
+  __syncthreads();
+  for (int b0 = 0; b0 < batch; b0 += 256) {
+    const int i = b0 + tid;
+    const int cnt = i < batch ? (int)(((long)(cu_q[i + 1] - cu_q[i]) * group + PR - 1) / PR) : 0;
+    scan[tid] = cnt;
+    __syncthreads();
+    for (int off = 1; off < 256; off <<= 1) {  // inclusive scan
+      const int v = tid >= off ? scan[tid - off] : 0;
+      __syncthreads();
+      scan[tid] += v;
+      __syncthreads();
+    }
+    const int start = carry + scan[tid] - cnt;
+    for (int t = 0; t < cnt && start + t < n_items; ++t) items[start + t] = make_int2(i, t);
+    __syncthreads();
+    if (tid == 255) carry += scan[255];
+    __syncthreads();
+  }
+  for (int k = carry + tid; k < n_items; k += 256) items[k] = make_int2(-1, 0);
+}
+
 __global__ void __launch_bounds__(256)
 store_kvcache_kernel(const uint16_t* __restrict__ key, long key_stride, const uint16_t* __restrict__ value,
                      long value_stride, uint16_t* __restrict__ k_cache, uint16_t* __restrict__ v_cache,
@@ -330,17 +390,40 @@ store_kvcache_kernel(const uint16_t* __restrict__ key, long key_stride, const ui
 
 }  // namespace
 
-// keys per workgroup for a longest sequence of max_k keys: PCH, widened so a row
-// has at most kMaxChunks chunks
-int chunk_keys(int max_k) {
+// The work split of one call: items (row tiles) bounded by the padded count
+// batch * ceil(max_q * G / 32) and, when the host knows the number of query
+// rows, by ceil(total_q * G / 32) + batch; chunks of keys so that items x KV
+// heads x chunks is about kTargetWaves (at most ceil(max_k / 256) chunks, and a
+// row has at most kMaxChunks of them: wider chunks past 32 K keys).
+struct PagedPlan {
+  long n_items;
+  int n_chunks, chunk;
+};
+PagedPlan paged_plan(int batch, int kv_heads, int group, int max_q, int max_k, long total_q) {
+  PagedPlan p;
+  p.n_items = (long)batch * (((long)max_q * group + PR - 1) / PR);
+  if (total_q > 0) {
+    const long bound = (total_q * group + PR - 1) / PR + batch;
+    if (bound < p.n_items) p.n_items = bound;
+  }
   const long units = ((long)max_k + PCH - 1) / PCH;
-  return (int)((units + kMaxChunks - 1) / kMaxChunks) * PCH;
+  long nc = (kTargetWaves + p.n_items * kv_heads - 1) / (p.n_items * kv_heads);
+  if (nc > units) nc = units;
+  if (nc < 1) nc = 1;
+  long per = (units + nc - 1) / nc;                                  // 256-key units per chunk
+  const long min_per = (units + kMaxChunks - 1) / kMaxChunks;        // at most kMaxChunks chunks
+  if (per < min_per) per = min_per;
+  p.chunk = (int)(per * PCH);
+  p.n_chunks = (int)((max_k + p.chunk - 1) / p.chunk);
+  return p;
 }
 
-long paged_attention_ws_floats(int batch, int kv_heads, int group, int max_q, int max_k, int head_dim) {
-  const long n_tiles = ((long)max_q * group + PR - 1) / PR;
-  const long n_chunks = ((long)max_k + chunk_keys(max_k) - 1) / chunk_keys(max_k);
-  return (long)batch * n_tiles * kv_heads * n_chunks * (2 * PR + (long)PR * head_dim);
+// workspace bytes: the item list (16-B aligned), then the partial sums when a row has several chunks
+long paged_attention_ws_bytes(int batch, int kv_heads, int group, int max_q, int max_k, int head_dim, long total_q) {
+  const PagedPlan p = paged_plan(batch, kv_heads, group, max_q, max_k, total_q);
+  const long list = (p.n_items * 8 + 255) / 256 * 256;
+  const long parts = p.n_chunks > 1 ? p.n_items * kv_heads * p.n_chunks * (2 * PR + (long)PR * head_dim) * 4 : 0;
+  return list + parts;
 }
 
 hipError_t paged_attention(const PagedAttnArgs& x, hipStream_t s) {
@@ -353,22 +436,27 @@ hipError_t paged_attention(const PagedAttnArgs& x, hipStream_t s) {
   a.cu_q = x.cu_q; a.cu_k = x.cu_k; a.seqlens_k = x.seqlens_k;
   a.block_table = x.block_table; a.bt_stride = x.bt_stride; a.block_size = x.block_size;
   a.out = x.out; a.out_stride = x.out_stride;
-  a.ws = x.ws;
   a.kv_heads = x.kv_heads;
   a.group = x.heads / x.kv_heads;
-  a.n_tiles = (int)(((long)x.max_q * a.group + PR - 1) / PR);
-  a.chunk = chunk_keys(x.max_k);
-  a.n_chunks = (x.max_k + a.chunk - 1) / a.chunk;
+  const PagedPlan p = paged_plan(x.batch, x.kv_heads, a.group, x.max_q, x.max_k, x.total_q);
+  a.chunk = p.chunk;
+  a.n_chunks = p.n_chunks;
+  const long list = (p.n_items * 8 + 255) / 256 * 256;
+  a.items = reinterpret_cast<const int2*>(x.ws);
+  a.ws = reinterpret_cast<float*>(reinterpret_cast<char*>(x.ws) + list);
   a.scale_log2 = x.scale * 1.4426950408889634f;
   a.causal = x.causal;
-  const long items = (long)x.batch * a.n_tiles;
-  if (items * a.n_chunks > 0x7fffffffL || x.kv_heads > 65535) return hipErrorInvalidValue;
-  const dim3 grid((unsigned)(items * a.n_chunks), (unsigned)x.kv_heads);
-  const dim3 cgrid((unsigned)items, (unsigned)x.kv_heads, kCombineSplit);
+  if (p.n_items * a.n_chunks > 0x7fffffffL || x.kv_heads > 65535) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(paged_plan_kernel, dim3(1), dim3(256), 0, s, x.cu_q, x.batch, a.group, (int)p.n_items,
+                     reinterpret_cast<int2*>(x.ws));
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  const dim3 grid((unsigned)(p.n_items * a.n_chunks), (unsigned)x.kv_heads);
+  const dim3 cgrid((unsigned)p.n_items, (unsigned)x.kv_heads, kCombineSplit);
   auto run = [&](auto attn, auto combine) {
     dfh_launch(attn, grid, dim3(64), 0, s, a);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
+    hipError_t e2 = hipGetLastError();
+    if (e2 != hipSuccess || a.n_chunks == 1) return e2;
     hipLaunchKernelGGL(combine, cgrid, dim3(256), 0, s, a);
     return hipGetLastError();
   };

@@ -97,10 +97,10 @@ def _run(q, k, v, *, cu_q, max_q, max_k, cu_k=None, seqlens_k=None, block_table=
         kv_stride=kv_stride, cu_seqlens_k=_lib.ptr(cu_k), seqlens_k=_lib.ptr(seqlens_k), block_table=_lib.ptr(bt),
         block_table_stride=bt.shape[1] if bt is not None else 0, block_size=int(block_size),
         out=_lib.ptr(out), out_stride=out.stride(0), softmax_scale=float(hd ** -0.5 if scale is None else scale),
-        causal=int(bool(causal)), workspace=None, workspace_bytes=0)
+        causal=int(bool(causal)), workspace=None, workspace_bytes=0, total_q=total_q)
     lib = _lib.lib()
     need = lib.dfh_paged_attention_workspace(C.byref(args))
-    ws = torch.empty(max(need // 4, 1), device=q.device, dtype=torch.float32)
+    ws = torch.empty(max((need + 3) // 4, 64), device=q.device, dtype=torch.float32)
     args.workspace = _lib.ptr(ws)
     args.workspace_bytes = ws.numel() * 4
     _lib.check(lib.dfh_paged_attention(C.byref(args), _lib.stream_ptr()), "dfh_paged_attention")

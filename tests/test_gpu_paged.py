@@ -1,8 +1,9 @@
 """Paged KV cache of the LLM backbone on the GPU (store_kvcache, paged /
 varlen attention) against the float64 oracle. GPU only.
 
-Bar: store_kvcache bit-exact; attention outputs (bf16) within 1e-2 absolute of
-the float64 oracle on the same bf16 inputs, and per-row cosine >= 0.99999."""
+Bar: store_kvcache bit-exact; attention outputs (bf16) within 1e-2 + 2^-8 |ref|
+of the float64 oracle on the same bf16 inputs (the bf16 output rounding is up to
+2^-9 |ref|, and P enters the P.V product in bf16), and per-row cosine >= 0.99999."""
 from __future__ import annotations
 
 import pytest
@@ -13,6 +14,7 @@ from oracle import paged_attn_ref as P
 pytestmark = pytest.mark.gpu
 
 ATOL = 1e-2
+RTOL = 2.0 ** -8
 COS = 0.99999
 
 
@@ -22,10 +24,12 @@ def _bf(x):
 
 def _check(got, ref, label):
     got = got.float().cpu().double()
-    err = (got - ref).abs().max().item()
+    diff = (got - ref).abs()
+    err = diff.max().item()
+    excess = (diff - (ATOL + RTOL * ref.abs())).max().item()
     c = torch.nn.functional.cosine_similarity(got.reshape(-1, got.shape[-1]), ref.reshape(-1, ref.shape[-1]), dim=-1)
     print(f"{label}: max abs {err:.3g}, cos min {c.min().item():.7f}", flush=True)
-    assert err <= ATOL, label
+    assert excess <= 0, f"{label}: {excess:.3g} over the bar"
     assert c.min().item() >= COS, label
 
 
@@ -104,6 +108,65 @@ def test_prefill_contiguous_matches_oracle(causal):
                                  causal=causal)
     ref = P.attention(q.cpu(), k.cpu(), v.cpu(), cu, cu_k=cu, scale=0.1, causal=causal)
     _check(out, ref, f"prefill-{causal}")
+
+
+def _ws_bytes(B, H, Hkv, hd, max_q, max_k, total_q):
+    import ctypes as C
+
+    from nanovllm_dots_amd import _lib
+    a = _lib.DfhPagedAttnArgs(batch=B, num_heads=H, num_kv_heads=Hkv, head_dim=hd, max_seqlen_q=max_q,
+                              max_seqlen_k=max_k, total_q=total_q)
+    return _lib.lib().dfh_paged_attention_workspace(C.byref(a))
+
+
+def test_mixed_prefill_workspace_sized_by_rows():
+    """One long prompt and many short ones in one prefill (the scheduler's
+    16384-token budget allows 4096 + 511 x 24): the workspace follows the
+    batch's query rows, not batch x the longest prompt, and the output matches."""
+    from nanovllm_dots_amd.paged_attention import flash_attn_varlen_func
+    H, Hkv, hd = 12, 2, 128
+    # the scheduler's worst case (sizes only, no launch): 3,580 row tiles x 2 KV heads fill the GPU, so
+    # one chunk per tile and only the item list; a 32 K-token prompt alike
+    sized = _ws_bytes(512, H, Hkv, hd, 4096, 4096, 4096 + 511 * 24)
+    long_prompt = _ws_bytes(1, H, Hkv, hd, 32768, 32768, 32768)
+    # decode of 512 sequences at 4096 keys keeps the split (partial sums of 16.6 KB per row tile and chunk)
+    decode = _ws_bytes(512, H, Hkv, hd, 1, 4096, 512)
+    print(f"workspace: 4096 + 511 x 24 prefill {sized / 2**10:.1f} KiB, 32 K prompt {long_prompt / 2**10:.1f} KiB, "
+          f"512-sequence decode {decode / 2**20:.1f} MiB", flush=True)
+    assert sized < 2**20 and long_prompt < 2**20 and decode < 2**28
+    # a smaller instance of the same shape, run against the oracle
+    lens = [1500] + [24] * 60
+    print(f"mixed prefill lens=[1500] + [24] x 60", flush=True)
+    g = torch.Generator().manual_seed(6)
+    tot = sum(lens)
+    q = _bf(torch.randn(tot, H, hd, generator=g))
+    k = _bf(torch.randn(tot, Hkv, hd, generator=g))
+    v = _bf(torch.randn(tot, Hkv, hd, generator=g))
+    cu = _cu(lens)
+    out = flash_attn_varlen_func(q, k, v, cu.cuda(), cu.cuda(), max(lens), max(lens), causal=True)
+    ref = P.attention(q.cpu(), k.cpu(), v.cpu(), cu, cu_k=cu, causal=True)
+    _check(out, ref, "mixed-prefill")
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_prefill_one_chunk_direct_output(causal):
+    """Row tiles alone fill the GPU: one chunk per tile, the attention kernel
+    writes the normalised rows itself (no partial sums, no combine), and the
+    workspace holds only the item list."""
+    from nanovllm_dots_amd.paged_attention import flash_attn_varlen_func
+    H, Hkv, hd = 32, 32, 64
+    lens = [1500, 1400, 1600, 3]
+    tot = sum(lens)
+    assert _ws_bytes(len(lens), H, Hkv, hd, max(lens), max(lens), tot) < 4096
+    print(f"direct prefill causal={causal} lens={lens}", flush=True)
+    g = torch.Generator().manual_seed(7)
+    q = _bf(torch.randn(tot, H, hd, generator=g))
+    k = _bf(torch.randn(tot, Hkv, hd, generator=g))
+    v = _bf(torch.randn(tot, Hkv, hd, generator=g))
+    cu = _cu(lens)
+    out = flash_attn_varlen_func(q, k, v, cu.cuda(), cu.cuda(), max(lens), max(lens), causal=causal)
+    ref = P.attention(q.cpu(), k.cpu(), v.cpu(), cu, cu_k=cu, causal=causal)
+    _check(out, ref, f"direct-prefill-{causal}")
 
 
 def test_decode_long_context_and_contiguous_cache():
