@@ -174,7 +174,7 @@ int dfh_set_latent_tail(DfhHandle* h, int enable);
 int dfh_profile_read(DfhHandle* h, double* ms_per_class, long* launches_per_class, int n_classes);
 
 /* Standalone bf16 GEMM: C[M,N] = A[M,K] B[N,K]^T + bias (bias may be NULL).
- * epilogue: 0 bf16 out, 1 GELU(tanh) bf16 out, 4 float32 out. */
+ * epilogue: 0 bf16 out, 1 GELU(tanh) bf16 out, 4 float32 out, 7 SiLU bf16 out. */
 int dfh_gemm_bf16(const void* A, long lda, const void* B, long ldb, void* C, long ldc,
                   const void* bias, int M, int N, int K, int epilogue, int tile, void* stream);
 /* dfh_gemm_bf16 with a device workspace (ws, ws_bytes) for the K-split of the
@@ -272,6 +272,56 @@ typedef struct DfhPagedAttnArgs {
 } DfhPagedAttnArgs;
 long dfh_paged_attention_workspace(const DfhPagedAttnArgs* a);
 int dfh_paged_attention(const DfhPagedAttnArgs* a, void* stream);
+
+/* The patch encoder's per-patch decode (VAESemanticEncoder.decode_patch,
+ * nanovllm_dots/models/dots/native/patch_encoder.py:198-215) for n requests at
+ * once, request i in cache row rows[i] at that row's own history length:
+ * FlashPatchEncoder (nanovllm_dots/models/dots/flash_patch_encoder.py:35-139).
+ * A handle owns the packed bf16 weights, per layer a K and a V cache of
+ * max_batch rows x capacity tokens x hidden, per row a conv tail (the last
+ * latent frame of its previous patch) and a length, and the workspace. Encoder
+ * layers: LayerNorm (affine) -> q, k, v without bias -> K / V appended at the
+ * row's length -> causal attention over the row's keys -> o_proj -> residual ->
+ * LayerNorm -> fc1 -> SiLU -> fc2 -> residual (native/patch_encoder.py:28-85,
+ * native/layers.py:210-249). Requirements: hidden a multiple of 256, head_dim
+ * 64 or 128, latent_dim a multiple of 32, patch even, out_dim and ffn multiples
+ * of 64; capacity is rounded up to a multiple of 256 tokens. */
+typedef struct DfhPatchEncConfig {
+  int latent_dim, patch, hidden, heads, ffn, n_layers, out_dim;
+  int max_batch;                    /* cache rows */
+  int capacity;                     /* tokens per row: max patches * patch / 2 */
+  float ln_eps;                     /* 1e-5 */
+} DfhPatchEncConfig;
+/* device bf16 parameters in nn.Linear [out, in] layout (state-dict names
+ * encoder.layers.{l}.attn.{q,k,v,o}_proj, attn_norm, ffn_norm, ffn.fc1, ffn.fc2) */
+typedef struct DfhPatchEncLayerWeights {
+  const void *attn_norm_w, *attn_norm_b, *q_w, *k_w, *v_w, *o_w, *o_b;
+  const void *ffn_norm_w, *ffn_norm_b, *fc1_w, *fc1_b, *fc2_w, *fc2_b;
+} DfhPatchEncLayerWeights;
+/* ds_w: ds_proj.weight [latent_dim, latent_dim, 2]; in_w: in_proj [hidden,
+ * latent_dim]; out_w: out_proj [out_dim, hidden * patch / 2] */
+typedef struct DfhPatchEncWeights {
+  const void *ds_w, *ds_b, *in_w, *in_b, *out_w, *out_b;
+  const DfhPatchEncLayerWeights* layers;   /* host array [n_layers] */
+} DfhPatchEncWeights;
+typedef struct DfhPatchEnc DfhPatchEnc;
+/* <- FlashPatchEncoder.__init__ (flash_patch_encoder.py:43-62): copies the
+ * weights, allocates the caches (rows at length 0, zero tails). */
+int dfh_patchenc_create(const DfhPatchEncConfig* cfg, const DfhPatchEncWeights* w, DfhPatchEnc** out);
+int dfh_patchenc_destroy(DfhPatchEnc* h);
+/* <- FlashPatchEncoder.reset_rows (flash_patch_encoder.py:64-69): rows (device
+ * int32 [n]) back to length 0 and a zero conv tail. */
+int dfh_patchenc_reset_rows(DfhPatchEnc* h, const int* rows, int n, void* stream);
+/* <- FlashPatchEncoder.decode_patch (flash_patch_encoder.py:103-139): patches
+ * [n, patch, latent_dim] bf16 (row stride patch_stride elements between
+ * requests), rows device int32 [n], distinct -> out [n, out_dim] bf16; each
+ * row's length advances by patch / 2. A row that would pass its capacity
+ * appends nothing and raises the overflow flag of dfh_patchenc_lengths. */
+int dfh_patchenc_decode(DfhPatchEnc* h, const void* patches, long patch_stride, const int* rows, int n, void* out,
+                        void* stream);
+/* lengths of all max_batch rows and the overflow flag (then cleared), copied to
+ * the host after the device finishes its queued work (synchronizes) */
+int dfh_patchenc_lengths(DfhPatchEnc* h, int* lengths, int* overflow);
 
 #ifdef __cplusplus
 }

@@ -6,5 +6,7 @@ behind the reference's accelerator entry points (``fm_accel="hip"``).
 from .hip_meanflow import (FMSpec, HipDiT, HipFMCache, HipFMHead, HipMeanflow, batched_meanflow,  # noqa: F401
                            meanflow_grid, rope_inv_freq, timestep_freqs)
 
-__all__ = ["FMSpec", "HipDiT", "HipFMCache", "HipFMHead", "HipMeanflow", "batched_meanflow", "meanflow_grid",
+from .patch_encoder import HipPatchEncoder  # noqa: F401
+
+__all__ = ["HipPatchEncoder", "FMSpec", "HipDiT", "HipFMCache", "HipFMHead", "HipMeanflow", "batched_meanflow", "meanflow_grid",
            "rope_inv_freq", "timestep_freqs"]

@@ -67,6 +67,21 @@ class DfhPagedAttnArgs(C.Structure):
     ]
 
 
+class DfhPatchEncConfig(C.Structure):
+    _fields_ = [(n, C.c_int) for n in ("latent_dim", "patch", "hidden", "heads", "ffn", "n_layers", "out_dim",
+                                        "max_batch", "capacity")] + [("ln_eps", C.c_float)]
+
+
+class DfhPatchEncLayerWeights(C.Structure):
+    _fields_ = [(n, vp) for n in ("attn_norm_w", "attn_norm_b", "q_w", "k_w", "v_w", "o_w", "o_b", "ffn_norm_w",
+                                  "ffn_norm_b", "fc1_w", "fc1_b", "fc2_w", "fc2_b")]
+
+
+class DfhPatchEncWeights(C.Structure):
+    _fields_ = [(n, vp) for n in ("ds_w", "ds_b", "in_w", "in_b", "out_w", "out_b")] + [
+        ("layers", C.POINTER(DfhPatchEncLayerWeights))]
+
+
 class DfhForwardArgs(C.Structure):
     _fields_ = [
         ("n", C.c_int), ("total_len", C.c_int), ("x", vp), ("timesteps", vp), ("duration", vp),
@@ -109,6 +124,11 @@ SIGNATURES = {
     "dfh_kvcache_extend": (C.c_int, [vp, vp, C.c_int, C.POINTER(C.c_int), vp, C.POINTER(C.c_float),
                                      C.POINTER(C.c_float), vp]),
     "dfh_kvcache_solve": (C.c_int, [vp, vp, vp, vp, vp, C.POINTER(C.c_float), C.POINTER(C.c_float), vp]),
+    "dfh_patchenc_create": (C.c_int, [C.POINTER(DfhPatchEncConfig), C.POINTER(DfhPatchEncWeights), C.POINTER(vp)]),
+    "dfh_patchenc_destroy": (C.c_int, [vp]),
+    "dfh_patchenc_reset_rows": (C.c_int, [vp, vp, C.c_int, vp]),
+    "dfh_patchenc_decode": (C.c_int, [vp, vp, C.c_long, vp, C.c_int, vp, vp]),
+    "dfh_patchenc_lengths": (C.c_int, [vp, C.POINTER(C.c_int), C.POINTER(C.c_int)]),
 }
 
 _lib = None

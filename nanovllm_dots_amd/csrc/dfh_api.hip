@@ -828,7 +828,7 @@ int dfh_gemm_bf16(const void* A, long lda, const void* B, long ldb, void* C, lon
 int dfh_gemm_bf16_ws(const void* A, long lda, const void* B, long ldb, void* C, long ldc, const void* bias,
                      int M, int N, int K, int epilogue, int tile, void* ws, long ws_bytes, void* stream) {
   if (!A || !B || !C) return fail("dfh_gemm_bf16: NULL pointer");
-  if (epilogue != EPI_BIAS && epilogue != EPI_GELU && epilogue != EPI_F32)
+  if (epilogue != EPI_BIAS && epilogue != EPI_GELU && epilogue != EPI_SILU && epilogue != EPI_F32)
     return fail("dfh_gemm_bf16: epilogue %d not exposed", epilogue);
   if (lda % 8 || ldb % 8 || ldc % 8 || lda < K || ldb < K || ldc < N)
     return fail("dfh_gemm_bf16: leading dimensions must be >= the row length and multiples of 8");
@@ -1218,6 +1218,214 @@ int dfh_kvcache_solve(DfhKVCache* c, const void* last_hidden, const void* g_cond
   return cache_solve(c, reinterpret_cast<const uint16_t*>(last_hidden), nullptr,
                      reinterpret_cast<const uint16_t*>(g_cond), reinterpret_cast<const uint16_t*>(noise),
                      reinterpret_cast<uint16_t*>(out), tv, dtv, max_len, reinterpret_cast<hipStream_t>(stream));
+}
+
+}  // extern "C"
+
+// ----------------------------------------------------------------------------
+// Patch encoder decode (FlashPatchEncoder.decode_patch, flash_patch_encoder.py
+// :103-139). Per call, stream-ordered: per-call tables (K/V slots, key counts,
+// query offsets) from the rows' lengths; causal downsample of each request's
+// patch (conv tail in, new tail out) and in_proj; per layer LayerNorm, fused
+// q|k|v GEMM, K / V rows appended to the cache, paged attention with one page
+// per cache row (block_table = rows), o_proj with an in-place residual add,
+// LayerNorm, fc1 + SiLU, fc2 with an in-place residual add; the rows' lengths
+// advance; out_proj over each request's patch / 2 tokens side by side.
+// ----------------------------------------------------------------------------
+struct DfhPatchEnc {
+  DfhPatchEncConfig cfg;
+  int ods = 0, cap = 0;
+  DevBuf arena;  // packed weights
+  const uint16_t *ds_w, *ds_b, *in_w, *in_b, *out_w, *out_b;
+  std::vector<const uint16_t*> ln1_w, ln1_b, qkv_w, o_w, o_b, ln2_w, ln2_b, fc1_w, fc1_b, fc2_w, fc2_b;
+  DevBuf kc, vc;                 // [n_layers][max_batch * cap][hidden]
+  DevBuf len, tail, err;         // per row: length, conv tail [latent_dim]; overflow flag
+  DevBuf x, hb, qkv, attn, ff, conv, slots, seqk, cuq, zeros, ones, paws;
+  DevBuf rows_ok;                // the call's rows, out-of-range entries replaced by row 0
+};
+
+namespace {
+int pe_gemm(const uint16_t* A, long lda, const uint16_t* B, const uint16_t* bias, uint16_t* C, long ldc, int M,
+            int N, int K, int epi, const DfhPatchEnc* h, hipStream_t s) {
+  GemmArgs a;
+  memset(&a, 0, sizeof(a));
+  a.A = A; a.lda = lda; a.B = B; a.ldb = K; a.C = C; a.ldc = ldc; a.bias = bias;
+  a.M = M; a.N = N; a.K = K;
+  if (epi == EPI_GATE_RES) {  // x += bf16(acc + bias): unit gate for every row
+    a.gate = P<const uint16_t>(const_cast<DevBuf&>(h->ones)); a.ld_gate = 0;
+    a.row_req = P<const int>(const_cast<DevBuf&>(h->zeros));
+  }
+  hipError_t e = gemm_bf16(a, epi, s, -1);
+  if (e != hipSuccess) return fail("patch encoder GEMM (M=%d N=%d K=%d epi=%d): %s", M, N, K, epi, hipGetErrorString(e));
+  return 0;
+}
+}  // namespace
+
+extern "C" {
+
+int dfh_patchenc_create(const DfhPatchEncConfig* cfg, const DfhPatchEncWeights* w, DfhPatchEnc** out) {
+  if (!cfg || !w || !out || !w->layers) return fail("dfh_patchenc_create: NULL argument");
+  const DfhPatchEncConfig& c = *cfg;
+  if (c.hidden <= 0 || c.heads <= 0 || c.hidden % c.heads || c.hidden % 256)
+    return fail("dfh_patchenc_create: hidden %d must be a positive multiple of 256 and of heads %d", c.hidden,
+                c.heads);
+  const int hd = c.hidden / c.heads;
+  if (hd != 64 && hd != 128) return fail("dfh_patchenc_create: head_dim %d not supported (64 or 128)", hd);
+  if (c.latent_dim <= 0 || c.latent_dim % 32 || c.patch <= 0 || c.patch % 2 || c.out_dim <= 0 || c.out_dim % 64 ||
+      c.ffn <= 0 || c.ffn % 64 || c.n_layers <= 0 || c.max_batch <= 0 || c.capacity <= 0)
+    return fail("dfh_patchenc_create: bad shape (latent_dim %d, patch %d, ffn %d, out_dim %d, layers %d, rows %d, "
+                "capacity %d)", c.latent_dim, c.patch, c.ffn, c.out_dim, c.n_layers, c.max_batch, c.capacity);
+  if ((long)(c.patch + 1) * c.latent_dim * 4 > 64 * 1024) return fail("dfh_patchenc_create: patch too large");
+  auto* h = new DfhPatchEnc();
+  h->cfg = c;
+  h->ods = c.patch / 2;
+  h->cap = (c.capacity + 255) / 256 * 256;
+  const long H = c.hidden, F = c.ffn, L = c.latent_dim, rows_max = (long)c.max_batch * h->ods;
+  auto fail_free = [&](int rc) {
+    dfh_patchenc_destroy(h);
+    return rc;
+  };
+  // weight arena: 256-B aligned pieces
+  std::vector<std::pair<const void*, long>> pieces;  // (source, elements)
+  auto add = [&](const void* src, long n) { pieces.push_back({src, n}); };
+  add(w->ds_w, L * L * 2); add(w->ds_b, L); add(w->in_w, H * L); add(w->in_b, H);
+  add(w->out_w, (long)c.out_dim * H * h->ods); add(w->out_b, c.out_dim);
+  for (int l = 0; l < c.n_layers; ++l) {
+    const DfhPatchEncLayerWeights& lw = w->layers[l];
+    add(lw.attn_norm_w, H); add(lw.attn_norm_b, H);
+    add(lw.q_w, H * H); add(lw.k_w, H * H); add(lw.v_w, H * H);  // consecutive: the fused [3H, H] q|k|v
+    add(lw.o_w, H * H); add(lw.o_b, H);
+    add(lw.ffn_norm_w, H); add(lw.ffn_norm_b, H);
+    add(lw.fc1_w, F * H); add(lw.fc1_b, F); add(lw.fc2_w, H * F); add(lw.fc2_b, H);
+  }
+  std::vector<long> offs;
+  long total = 0;
+  for (auto& p : pieces) {
+    if (!p.first) return fail_free(fail("dfh_patchenc_create: a weight pointer is NULL"));
+    offs.push_back(total);
+    total += p.second * 2;
+    total = (total + 255) / 256 * 256;
+  }
+  // q, k, v of a layer must be contiguous for the fused GEMM: their sizes (H*H*2 bytes) are multiples of 256
+  if (dev_alloc(h->arena, total) != hipSuccess) return fail_free(fail("dfh_patchenc_create: weight allocation"));
+  for (size_t i = 0; i < pieces.size(); ++i)
+    if (hipMemcpy(reinterpret_cast<char*>(h->arena.p) + offs[i], pieces[i].first, pieces[i].second * 2,
+                  hipMemcpyDeviceToDevice) != hipSuccess)
+      return fail_free(fail("dfh_patchenc_create: weight copy %zu failed", i));
+  auto at = [&](size_t i) { return reinterpret_cast<const uint16_t*>(reinterpret_cast<char*>(h->arena.p) + offs[i]); };
+  size_t k = 0;
+  h->ds_w = at(k++); h->ds_b = at(k++); h->in_w = at(k++); h->in_b = at(k++); h->out_w = at(k++); h->out_b = at(k++);
+  for (int l = 0; l < c.n_layers; ++l) {
+    h->ln1_w.push_back(at(k++)); h->ln1_b.push_back(at(k++));
+    h->qkv_w.push_back(at(k)); k += 3;
+    h->o_w.push_back(at(k++)); h->o_b.push_back(at(k++));
+    h->ln2_w.push_back(at(k++)); h->ln2_b.push_back(at(k++));
+    h->fc1_w.push_back(at(k++)); h->fc1_b.push_back(at(k++)); h->fc2_w.push_back(at(k++)); h->fc2_b.push_back(at(k++));
+  }
+  const size_t cache = (size_t)c.n_layers * c.max_batch * h->cap * H * 2;
+  // a call with fewer requests may split rows into more chunks: the largest need over every batch size
+  long pa_ws = 0;
+  for (int nb = 1; nb <= c.max_batch; ++nb) {
+    const long need = dfh::paged_attention_ws_bytes(nb, c.heads, 1, h->ods, h->cap, hd, (long)nb * h->ods);
+    pa_ws = need > pa_ws ? need : pa_ws;
+  }
+  std::vector<uint16_t> ones(H, 0x3f80);  // bf16 1.0
+  if (dev_alloc(h->kc, cache) || dev_alloc(h->vc, cache) || dev_alloc(h->len, (size_t)c.max_batch * 4) ||
+      dev_alloc(h->tail, (size_t)c.max_batch * L * 2) || dev_alloc(h->err, 256) ||
+      dev_alloc(h->x, rows_max * H * 2) || dev_alloc(h->hb, rows_max * H * 2) ||
+      dev_alloc(h->qkv, rows_max * 3 * H * 2) || dev_alloc(h->attn, rows_max * H * 2) ||
+      dev_alloc(h->ff, rows_max * F * 2) || dev_alloc(h->conv, rows_max * L * 2) ||
+      dev_alloc(h->slots, rows_max * 4) || dev_alloc(h->seqk, (size_t)c.max_batch * 4) ||
+      dev_alloc(h->cuq, (size_t)(c.max_batch + 1) * 4) || dev_alloc(h->zeros, rows_max * 4) ||
+      dev_alloc(h->ones, H * 2) || dev_alloc(h->paws, pa_ws > 0 ? pa_ws : 256) ||
+      dev_alloc(h->rows_ok, (size_t)c.max_batch * 4) ||
+      hipMemcpy(h->ones.p, ones.data(), H * 2, hipMemcpyHostToDevice))
+    return fail_free(fail("dfh_patchenc_create: allocation of %.1f MiB of caches failed", 2.0 * cache / (1 << 20)));
+  *out = h;
+  return 0;
+}
+
+int dfh_patchenc_destroy(DfhPatchEnc* h) {
+  if (!h) return 0;
+  (void)hipDeviceSynchronize();
+  for (DevBuf* b : {&h->arena, &h->kc, &h->vc, &h->len, &h->tail, &h->err, &h->x, &h->hb, &h->qkv, &h->attn, &h->ff,
+                    &h->conv, &h->slots, &h->seqk, &h->cuq, &h->zeros, &h->ones, &h->paws, &h->rows_ok})
+    if (b->p) (void)hipFree(b->p);
+  delete h;
+  return 0;
+}
+
+int dfh_patchenc_reset_rows(DfhPatchEnc* h, const int* rows, int n, void* stream) {
+  if (!h) return fail("dfh_patchenc_reset_rows: NULL handle");
+  if (n < 0 || n > h->cfg.max_batch || (n > 0 && !rows))
+    return fail("dfh_patchenc_reset_rows: %d rows (the handle has %d)", n, h->cfg.max_batch);
+  DFH_CHECK(pe_reset(rows, n, h->cfg.max_batch, P<int>(h->len), P<uint16_t>(h->tail), h->cfg.latent_dim,
+                     reinterpret_cast<hipStream_t>(stream)));
+  return 0;
+}
+
+int dfh_patchenc_decode(DfhPatchEnc* h, const void* patches, long patch_stride, const int* rows, int n, void* out,
+                        void* stream) {
+  if (!h) return fail("dfh_patchenc_decode: NULL handle");
+  if (n == 0) return 0;
+  if (n < 0 || n > h->cfg.max_batch)
+    return fail("dfh_patchenc_decode: %d requests (the handle has %d rows)", n, h->cfg.max_batch);
+  if (!patches || !rows || !out) return fail("dfh_patchenc_decode: NULL pointer");
+  const DfhPatchEncConfig& c = h->cfg;
+  if (patch_stride < (long)c.patch * c.latent_dim) return fail("dfh_patchenc_decode: patch_stride too small");
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const int H = c.hidden, F = c.ffn, L = c.latent_dim, ods = h->ods, M = n * ods;
+  const long lstride = (long)c.max_batch * h->cap * H;  // one layer's cache, elements
+  DFH_CHECK(pe_plan(rows, P<int>(h->len), n, ods, h->cap, c.max_batch, P<int>(h->rows_ok), P<int>(h->slots),
+                    P<int>(h->seqk), P<int>(h->cuq), P<int>(h->err), s));
+  rows = P<const int>(h->rows_ok);  // the caller's rows, range-checked
+  DFH_CHECK(pe_downsample(reinterpret_cast<const uint16_t*>(patches), patch_stride, h->ds_w, h->ds_b, rows,
+                          P<uint16_t>(h->tail), P<uint16_t>(h->conv), n, c.patch, L, s));
+  uint16_t* x = P<uint16_t>(h->x);
+  uint16_t* hb = P<uint16_t>(h->hb);
+  uint16_t* qkv = P<uint16_t>(h->qkv);
+  uint16_t* attn = P<uint16_t>(h->attn);
+  uint16_t* ff = P<uint16_t>(h->ff);
+  if (pe_gemm(P<uint16_t>(h->conv), L, h->in_w, h->in_b, x, H, M, H, L, EPI_BIAS, h, s)) return 1;
+  for (int l = 0; l < c.n_layers; ++l) {
+    uint16_t* kc = P<uint16_t>(h->kc) + l * lstride;
+    uint16_t* vc = P<uint16_t>(h->vc) + l * lstride;
+    DFH_CHECK(ln_affine(x, hb, h->ln1_w[l], h->ln1_b[l], M, H, c.ln_eps, s));
+    if (pe_gemm(hb, H, h->qkv_w[l], nullptr, qkv, 3 * H, M, 3 * H, H, EPI_BIAS, h, s)) return 1;
+    DFH_CHECK(store_kvcache(qkv + H, 3 * H, qkv + 2 * H, 3 * H, kc, vc, P<int>(h->slots), M, H, s));
+    PagedAttnArgs pa{};
+    pa.batch = n; pa.heads = c.heads; pa.kv_heads = c.heads; pa.head_dim = H / c.heads;
+    pa.max_q = ods; pa.max_k = h->cap; pa.total_q = M;
+    pa.q = qkv; pa.q_stride = 3 * H; pa.cu_q = P<int>(h->cuq);
+    pa.k = kc; pa.v = vc; pa.kv_stride = H; pa.cu_k = nullptr; pa.seqlens_k = P<int>(h->seqk);
+    pa.block_table = rows; pa.bt_stride = 1; pa.block_size = h->cap;
+    pa.out = attn; pa.out_stride = H; pa.scale = 1.0f / sqrtf((float)(H / c.heads)); pa.causal = 1;
+    pa.ws = h->paws.p;
+    if (dfh::paged_attention_ws_bytes(n, c.heads, 1, ods, h->cap, H / c.heads, M) > (long)h->paws.bytes)
+      return fail("dfh_patchenc_decode: attention workspace too small for %d requests", n);
+    DFH_CHECK(paged_attention(pa, s));
+    if (pe_gemm(attn, H, h->o_w[l], h->o_b[l], x, H, M, H, H, EPI_GATE_RES, h, s)) return 1;
+    DFH_CHECK(ln_affine(x, hb, h->ln2_w[l], h->ln2_b[l], M, H, c.ln_eps, s));
+    if (pe_gemm(hb, H, h->fc1_w[l], h->fc1_b[l], ff, F, M, F, H, EPI_SILU, h, s)) return 1;
+    if (pe_gemm(ff, F, h->fc2_w[l], h->fc2_b[l], x, H, M, H, F, EPI_GATE_RES, h, s)) return 1;
+  }
+  DFH_CHECK(pe_advance(rows, P<int>(h->len), n, ods, h->cap, s));
+  // request i's ods tokens are consecutive rows: one [n, ods * H] row each
+  if (pe_gemm(x, (long)ods * H, h->out_w, h->out_b, reinterpret_cast<uint16_t*>(out), c.out_dim, n, c.out_dim,
+              ods * H, EPI_BIAS, h, s))
+    return 1;
+  return 0;
+}
+
+int dfh_patchenc_lengths(DfhPatchEnc* h, int* lengths, int* overflow) {
+  if (!h) return fail("dfh_patchenc_lengths: NULL handle");
+  DFH_CHECK(hipDeviceSynchronize());
+  if (lengths) DFH_CHECK(hipMemcpy(lengths, h->len.p, (size_t)h->cfg.max_batch * 4, hipMemcpyDeviceToHost));
+  int e = 0;
+  DFH_CHECK(hipMemcpy(&e, h->err.p, 4, hipMemcpyDeviceToHost));
+  if (overflow) *overflow = e;
+  if (e) DFH_CHECK(hipMemset(h->err.p, 0, 4));
+  return 0;
 }
 
 }  // extern "C"

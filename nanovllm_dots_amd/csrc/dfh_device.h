@@ -88,6 +88,11 @@ __device__ __forceinline__ float gelu_tanh_f(float x) {
 }
 
 __device__ __forceinline__ float silu_f(float x) { return x / (1.0f + expf(-x)); }
+// x * sigmoid(x) = x / (1 + 2^(-x*log2(e))) with one exp2 and one reciprocal
+// (the GEMM epilogue's SiLU; within a few float32 ulp of silu_f)
+__device__ __forceinline__ float silu_fast(float x) {
+  return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-1.4426950408889634f * x));
+}
 
 // value of lane l ^ 32 (the other half of the wave): one v_permlane32_swap,
 // which exchanges lanes 32..63 of its first operand with lanes 0..31 of its

@@ -24,6 +24,7 @@ enum Epilogue : int {
   EPI_F32 = 4,       // Cf = acc + bias (float32 out; tests)
   EPI_I32 = 5,       // int8 operands: Ci = int32 accumulators
   EPI_DQ = 6,        // int8 operands: C = bf16(((float(acc) * sx[m]) * sw[n]) + bias[n])
+  EPI_SILU = 7,      // C = bf16(silu(bf16(acc + bias)))
 };
 
 struct GemmArgs {

@@ -49,4 +49,14 @@ hipError_t gather_rows(const uint16_t* src, const int* src_rows, const int* dst_
                        uint16_t* dst, hipStream_t s);
 hipError_t z_update(uint16_t* z, const uint16_t* v, float dt, long n, hipStream_t s);
 
+// patch encoder (patch_encoder.hip)
+hipError_t ln_affine(const uint16_t* x, uint16_t* out, const uint16_t* w, const uint16_t* b, int rows, int H,
+                     float eps, hipStream_t s);
+hipError_t pe_downsample(const uint16_t* patch, long patch_stride, const uint16_t* w, const uint16_t* bias,
+                         const int* rows, uint16_t* tail, uint16_t* out, int n, int P, int ld, hipStream_t s);
+hipError_t pe_plan(const int* rows, const int* len, int n, int ods, int cap, int max_rows, int* rows_ok, int* slots,
+                   int* seqlens_k, int* cu_q, int* err, hipStream_t s);
+hipError_t pe_advance(const int* rows, int* len, int n, int ods, int cap, hipStream_t s);
+hipError_t pe_reset(const int* rows, int n, int max_rows, int* len, uint16_t* tail, int ld, hipStream_t s);
+
 }  // namespace dfh

@@ -136,7 +136,7 @@ struct OpI8 {
 // 16 B per lane, one 32-row block ahead of the block it stores.
 template <class C, int EPI>
 struct Staged {
-  static constexpr bool kEpi = EPI == EPI_BIAS || EPI == EPI_GELU || EPI == EPI_GATE_RES;
+  static constexpr bool kEpi = EPI == EPI_BIAS || EPI == EPI_GELU || EPI == EPI_SILU || EPI == EPI_GATE_RES;
   static constexpr int kSmall = C::BM < C::BN ? C::BM : C::BN;
   static constexpr bool value = kEpi && (C::NW / 2) * 32 * C::WTN <= kSmall * C::BK && C::NW % 2 == 0;
   static constexpr int CPR = C::WTN / 8;   // 16-B chunks per staged row
@@ -279,6 +279,9 @@ __device__ __forceinline__ void staged_epilogue(const GemmArgs& a, ACC (&acc)[C:
         if constexpr (EPI == EPI_GELU) {
 #pragma unroll
           for (int t = 0; t < 4; ++t) y[t] = gelu_tanh_f(rbf(y[t]));
+        } else if constexpr (EPI == EPI_SILU) {
+#pragma unroll
+          for (int t = 0; t < 4; ++t) y[t] = silu_fast(rbf(y[t]));
         }
         *reinterpret_cast<uint2*>(region + stage_off<CPR>(l32, 4 * i + g) + 4 * hi) = pack4(y[0], y[1], y[2], y[3]);
       }
@@ -504,6 +507,9 @@ __device__ __forceinline__ void run_epilogue(const GemmArgs& a, ACC (&acc)[C::RN
             } else if constexpr (EPI == EPI_GELU) {
 #pragma unroll
               for (int t = 0; t < 4; ++t) y[t] = gelu_tanh_f(rbf(y[t]));
+            } else if constexpr (EPI == EPI_SILU) {
+#pragma unroll
+              for (int t = 0; t < 4; ++t) y[t] = silu_fast(rbf(y[t]));
             } else if constexpr (EPI == EPI_GATE_RES) {
               float gt[4], xr[4];
               unpack4(*reinterpret_cast<const uint2*>(grow + n), gt);
@@ -1170,6 +1176,7 @@ hipError_t gemm_bf16(const GemmArgs& a, int epi, hipStream_t s, int tile) {
   switch (epi) {
     case EPI_BIAS: return dispatch_tiles<OpBf16, EPI_BIAS>(a, s, tile);
     case EPI_GELU: return dispatch_tiles<OpBf16, EPI_GELU>(a, s, tile);
+    case EPI_SILU: return dispatch_tiles<OpBf16, EPI_SILU>(a, s, tile);
     case EPI_GATE_RES: return dispatch_tiles<OpBf16, EPI_GATE_RES>(a, s, tile);
     case EPI_QKV: return dispatch_tiles<OpBf16, EPI_QKV>(a, s, tile);
     case EPI_F32: return dispatch_tiles<OpBf16, EPI_F32>(a, s, tile);
