@@ -272,6 +272,16 @@ typedef struct DfhPagedAttnArgs {
 } DfhPagedAttnArgs;
 long dfh_paged_attention_workspace(const DfhPagedAttnArgs* a);
 int dfh_paged_attention(const DfhPagedAttnArgs* a, void* stream);
+/* No counterpart in the reference: dfh_paged_attention for callers that cannot
+ * allocate (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc). Same arguments and results; a->workspace and
+ * a->workspace_bytes are ignored and the library's static device scratch is
+ * used instead: 64 MiB per GPU, held until the process ends (a decode of 64
+ * sequences x 4096 keys, 2 KV heads of head_dim 128, needs 32.5 MiB). Calls whose
+ * dfh_paged_attention_workspace(a) exceeds 64 MiB fail with an error. Every
+ * call on a GPU shares that GPU's scratch: calls that overlap on one GPU (two
+ * streams, or two threads) race. No hipMalloc, hipFree or memset. */
+int dfh_paged_attention_noalloc(const DfhPagedAttnArgs* a, void* stream);
 
 /* The patch encoder's per-patch decode (VAESemanticEncoder.decode_patch,
  * nanovllm_dots/models/dots/native/patch_encoder.py:198-215) for n requests at

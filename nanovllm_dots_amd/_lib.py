@@ -117,6 +117,7 @@ SIGNATURES = {
     "dfh_store_kvcache": (C.c_int, [vp, C.c_long, vp, C.c_long, vp, vp, vp, C.c_int, C.c_int, vp]),
     "dfh_paged_attention_workspace": (C.c_long, [C.POINTER(DfhPagedAttnArgs)]),
     "dfh_paged_attention": (C.c_int, [C.POINTER(DfhPagedAttnArgs), vp]),
+    "dfh_paged_attention_noalloc": (C.c_int, [C.POINTER(DfhPagedAttnArgs), vp]),
     "dfh_kvcache_create": (C.c_int, [vp, C.c_int, C.c_int, C.c_int, C.POINTER(vp)]),
     "dfh_kvcache_destroy": (C.c_int, [vp]),
     "dfh_kvcache_reset": (C.c_int, [vp, vp]),

@@ -909,6 +909,21 @@ int dfh_paged_attention(const DfhPagedAttnArgs* a, void* stream) {
   return 0;
 }
 
+int dfh_paged_attention_noalloc(const DfhPagedAttnArgs* a, void* stream) {
+  if (!a) return fail("null argument");
+  const long need = dfh_paged_attention_workspace(a);
+  if (need > dfh::kPagedScratchBytes)
+    return fail("dfh_paged_attention_noalloc: this call needs %ld bytes of workspace, more than the %ld-byte static "
+                "scratch (use dfh_paged_attention with a workspace)", need, dfh::kPagedScratchBytes);
+  hipError_t e = hipSuccess;
+  void* ws = dfh::paged_scratch(&e);
+  if (!ws) return fail("dfh_paged_attention_noalloc: scratch address: %s", hipGetErrorString(e));
+  DfhPagedAttnArgs b = *a;
+  b.workspace = ws;
+  b.workspace_bytes = dfh::kPagedScratchBytes;
+  return dfh_paged_attention(&b, stream);
+}
+
 int dfh_quant_act_i8(const void* x, long ldx, void* q, long ldq, void* scale, int M, int K, void* stream) {
   if (!x || !q || !scale) return fail("dfh_quant_act_i8: NULL pointer");
   if (M < 0 || K <= 0 || K % 8 || ldx % 8 || ldq % 8 || ldx < K || ldq < K)

@@ -150,6 +150,10 @@ struct PagedAttnArgs {
 };
 long paged_attention_ws_bytes(int batch, int kv_heads, int group, int max_q, int max_k, int head_dim, long total_q);
 hipError_t paged_attention(const PagedAttnArgs& a, hipStream_t s);
+// the no-allocation entry point's workspace: a static device array of this size,
+// its address on the current device (looked up once per device)
+constexpr long kPagedScratchBytes = 64L << 20;
+void* paged_scratch(hipError_t* err);
 // key / value [n, D] rows (strides in elements) -> cache rows slots[i] ([num_slots, D]); slot < 0 skips
 hipError_t store_kvcache(const uint16_t* key, long key_stride, const uint16_t* value, long value_stride,
                          uint16_t* k_cache, uint16_t* v_cache, const int* slots, int n, int D, hipStream_t s);

@@ -38,12 +38,44 @@
 // With several chunks, each writes (max, sum, O) per row to the workspace and a
 // combine kernel merges the chunks of a row and writes bf16. Pages are multiples of 256
 // tokens, so a 64-key tile never straddles a page.
+#include <mutex>
 #include <type_traits>
 
 #include "dfh_device.h"
 #include "dfh_kernels.h"
 
+// Workspace of the no-allocation entry point (dfh_paged_attention_noalloc): a
+// file-scope device array, one copy per GPU at its own address, held until the
+// process ends. Host code uses the address hipGetSymbolAddress returns for the
+// current device (paged_scratch), never this name.
+static __device__ __align__(256) unsigned char scratch[dfh::kPagedScratchBytes];
+
 namespace dfh {
+
+void* paged_scratch(hipError_t* err) {
+  constexpr int kMaxDevices = 64;
+  static std::mutex mu;
+  static void* ptrs[kMaxDevices] = {};
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e == hipSuccess && (dev < 0 || dev >= kMaxDevices)) e = hipErrorInvalidDevice;
+  if (e != hipSuccess) {
+    *err = e;
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(mu);
+  if (!ptrs[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+      *err = e != hipSuccess ? e : hipErrorInvalidSymbol;
+      return nullptr;
+    }
+    ptrs[dev] = p;
+  }
+  *err = hipSuccess;
+  return ptrs[dev];
+}
 
 namespace {
 
