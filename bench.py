@@ -197,6 +197,42 @@ def w8a8_bench(reps: int = 20):
     return out
 
 
+def int8_solve_bench(mf, head, solve, ms_bf16: float, gemm_flops: float, steps: int, out_bf16):
+    """The same 64-request solve in W8A8 mode (the reference's quantize_dit_ DiT,
+    D/int8_dit.py; reported there as 2x slower than bf16 on A100): every DiT
+    linear with min(in, out) >= 512 as int8 x int8 -> int32 with per-token
+    activation quantisation and a dequantising epilogue. Latents against the
+    bf16 solve's are reported (the cost of W8A8 itself)."""
+    import torch
+    head.set_int8(True)
+    for _ in range(2):
+        out = solve()
+    torch.cuda.synchronize()
+    head.profile(True)
+    head.profile_read()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        out = solve()
+    e1.record()
+    torch.cuda.synchronize()
+    prof = head.profile_read()
+    head.profile(False)
+    head.set_int8(False)
+    ms = e0.elapsed_time(e1) / steps
+    a, b = out.float().reshape(-1, out.shape[-1]), out_bf16.float().reshape(-1, out.shape[-1])
+    cos = torch.nn.functional.cosine_similarity(a, b, dim=-1)
+    gemm_ms = sum(prof[k][0] for k in ("qkv_gemm", "o_gemm", "fc1_gemm", "fc2_gemm")) / steps
+    res = {"ms_per_solve": round(ms, 3), "speedup_vs_bf16": round(ms_bf16 / ms, 3),
+           "latent_xRT": round(out.shape[0] * out.shape[1] * FRAME_S / (ms * 1e-3), 1),
+           "gemm_tops": round(gemm_flops / (ms * 1e-3) / 1e12, 1),
+           "quantise_ms_per_solve": round(prof["quantise"][0] / steps, 3),
+           "per_class_ms": {k: round(v[0] / steps, 3) for k, v in prof.items()},
+           "latents_vs_bf16_cos_min": round(cos.min().item(), 6)}
+    log(f"int8 solve: {res}")
+    return res
+
+
 def power_bench(reps: int = 20):
     """The fc2 GEMM shape (M = 36937, N = 1024, K = 4096, bias epilogue) on two
     schedules (tile 8: 8 waves, 128x64 per wave; tile 9: 4 waves, 128x128 per
@@ -371,6 +407,7 @@ def main():
     ap.add_argument("--no-kvcache", action="store_true")
     ap.add_argument("--no-paged", action="store_true")
     ap.add_argument("--no-power", action="store_true")
+    ap.add_argument("--no-int8", action="store_true")
     ap.add_argument("--w8a8-only", action="store_true",
                     help="run only the W8A8 linears leg (M = 16384, four (K, N) shapes) and print its record")
     ap.add_argument("--kvcache-only", action="store_true",
@@ -476,6 +513,7 @@ def main():
                                                + per_launch["fc1_gemm"] + per_launch["fc2_gemm"])
     log("per-class ms/solve: " + ", ".join(f"{k}={v['ms_per_solve']:.3f}" for k, v in breakdown.items()))
 
+    i8 = None if args.no_int8 else int8_solve_bench(mf, head, solve, ms, gemm_flops, max(3, args.steps // 2), out)
     vl = varlen_bench(mf, hist, noise_d, g_d, out)
     pg = None if args.no_paged else paged_bench()
     w8 = None if args.no_w8a8 else w8a8_bench()
@@ -519,6 +557,7 @@ def main():
         "varlen_solve": vl,
         "llm_paged_attention": pg,
         "gemm_power_limit_fc2_shape": pw,
+        "int8_w8a8_solve": i8,
         "cpu_baseline": ({k: (round(v, 5) if isinstance(v, float) else v) for k, v in cpu.items()
                           if k in ("value", "unit", "cores", "kind", "sample")} if cpu else None),
         "cpu_xRT": round(cpu["xRT"], 4) if cpu else None,

@@ -177,6 +177,28 @@ int dfh_profile_read(DfhHandle* h, double* ms_per_class, long* launches_per_clas
  * epilogue: 0 bf16 out, 1 GELU(tanh) bf16 out, 4 float32 out, 7 SiLU bf16 out. */
 int dfh_gemm_bf16(const void* A, long lda, const void* B, long ldb, void* C, long ldc,
                   const void* bias, int M, int N, int K, int epilogue, int tile, void* stream);
+/* W8A8 mode of dfh_meanflow_solve / dfh_meanflow_solve_varlen / dfh_dit_forward
+ * and the cached solve <- quantize_dit_ + Int8DynamicLinear
+ * (nanovllm_dots/models/dots/int8_dit.py:34-85). Every DiT linear with
+ * min(in, out) >= 512 becomes W8A8: input_layer, the second linear of the time
+ * and duration MLPs, every adaLN (stacked as in DfhWeights), q|k|v (fused), o,
+ * fc1 and fc2. Per-output-channel int8 weights (float32 scales) come from the
+ * caller (w, any entry NULL: quantised here from the handle's bf16 weights
+ * exactly as Int8DynamicLinear does); the input rows of each linear are
+ * quantised per token in bf16 right before its int8 GEMM, whose int32
+ * accumulators are dequantised ((acc * s_x) * s_w) + b in the epilogue.
+ * enable = 0 returns to bf16. dfh_set_weights turns the mode off. */
+typedef struct DfhInt8Linear {
+  const void* w;       /* int8 [out, in] row-major, device */
+  const float* scale;  /* float32 [out], device */
+} DfhInt8Linear;
+typedef struct DfhInt8Weights {
+  DfhInt8Linear input, t_mlp2, d_mlp2;
+  DfhInt8Linear ada;                            /* [n_blocks * 6H + 2H, H] */
+  const DfhInt8Linear *qkv, *o, *fc1, *fc2;     /* host arrays [n_blocks]; qkv [3H, H] */
+} DfhInt8Weights;
+int dfh_set_int8(DfhHandle* h, int enable, const DfhInt8Weights* w, void* stream);
+
 /* dfh_gemm_bf16 with a device workspace (ws, ws_bytes) for the K-split of the
  * last partial round of tiles (see dfh_set_ksplit); too small or NULL: no split.
  * ws_bytes >= 4 * (4096 + 65536 * (number of CUs)) always suffices. The workspace must be

@@ -82,6 +82,15 @@ class DfhPatchEncWeights(C.Structure):
         ("layers", C.POINTER(DfhPatchEncLayerWeights))]
 
 
+class DfhInt8Linear(C.Structure):
+    _fields_ = [("w", vp), ("scale", vp)]
+
+
+class DfhInt8Weights(C.Structure):
+    _fields_ = [("input", DfhInt8Linear), ("t_mlp2", DfhInt8Linear), ("d_mlp2", DfhInt8Linear),
+                ("ada", DfhInt8Linear)] + [(n, C.POINTER(DfhInt8Linear)) for n in ("qkv", "o", "fc1", "fc2")]
+
+
 class DfhForwardArgs(C.Structure):
     _fields_ = [
         ("n", C.c_int), ("total_len", C.c_int), ("x", vp), ("timesteps", vp), ("duration", vp),
@@ -103,6 +112,7 @@ SIGNATURES = {
     "dfh_profile_enable": (C.c_int, [vp, C.c_int]),
     "dfh_set_ksplit": (C.c_int, [vp, C.c_int]),
     "dfh_set_latent_tail": (C.c_int, [vp, C.c_int]),
+    "dfh_set_int8": (C.c_int, [vp, C.c_int, vp, vp]),
     "dfh_profile_read": (C.c_int, [vp, C.POINTER(C.c_double), C.POINTER(C.c_long), C.c_int]),
     "dfh_gemm_bf16": (C.c_int, [vp, C.c_long, vp, C.c_long, vp, C.c_long, vp, C.c_int, C.c_int,
                                 C.c_int, C.c_int, C.c_int, vp]),

@@ -70,7 +70,13 @@ hipError_t dev_alloc(DevBuf& b, size_t bytes) {
 template <typename T>
 T* P(DevBuf& b) { return reinterpret_cast<T*>(b.p); }
 
-enum ProfClass { PC_QKV = 0, PC_O, PC_FC1, PC_FC2, PC_ATTN, PC_LN, PC_OTHER, PC_TAIL, PC_N };
+enum ProfClass { PC_QKV = 0, PC_O, PC_FC1, PC_FC2, PC_ATTN, PC_LN, PC_OTHER, PC_TAIL, PC_QUANT, PC_N };
+
+// an int8 linear: weight [N, K] row-major and its per-output-channel scales
+struct Q8 {
+  const int8_t* w = nullptr;
+  const float* s = nullptr;
+};
 
 }  // namespace
 
@@ -102,6 +108,17 @@ struct DfhHandle {
   DevBuf attq;     // attention work list: item count, then one AttnItem per 128-query tile
   bool ksplit = true;
   bool latent_tail = true;  // solve: the last block's attention / O / MLP on the latent rows only
+
+  // W8A8 mode (Int8DynamicLinear / quantize_dit_, int8_dit.py:34-85): every DiT
+  // linear with min(in, out) >= 512 has an int8 weight with per-output-channel
+  // scales; the input rows of each are quantised per token right before its GEMM
+  // (the q, k and v projections share their input and with it its quantisation)
+  bool int8 = false;
+  DevBuf w8;                          // the int8 weights and scales
+  Q8 in_q, t2_q, d2_q, ada_q;         // input_layer, time / duration MLP second linears, stacked adaLN
+  std::vector<Q8> qkv_q, o_q, fc1_q, fc2_q;
+  DevBuf aq, asx;                     // quantised input rows of the current GEMM and their scales
+  long aq_rows = 0;
 
   // profiling
   bool prof = false;
@@ -147,6 +164,44 @@ hipError_t gemm(DfhHandle* h, int pc, const GemmArgs& a_in, int epi, hipStream_t
     a.ws_elems = (long)(h->splitws.bytes / 4);
   }
   return gemm_bf16(a, epi, s, tile);
+}
+
+// int8 mode: room for the quantised input rows of any GEMM on `rows` rows (K <= max(hidden, ffn))
+int reserve_q8(DfhHandle* h, long rows, hipStream_t s) {
+  if (!h->int8 || rows <= h->aq_rows) return 0;
+  DFH_CHECK(hipStreamSynchronize(s));
+  const long K = h->cfg.ffn > h->cfg.hidden ? h->cfg.ffn : h->cfg.hidden;
+  DFH_CHECK(dev_alloc(h->aq, rows * K));
+  DFH_CHECK(dev_alloc(h->asx, rows * 4));
+  h->aq_rows = rows;
+  return 0;
+}
+
+// A linear layer: the bf16 GEMM, or in int8 mode with an int8 weight q, the
+// input rows quantised per token (bit-exact with int8_dit.py:57-58) and the i8
+// GEMM with the epilogue that dequantises first ((acc * s_x) * s_w) + b.
+hipError_t lin(DfhHandle* h, int pc, const GemmArgs& a, int epi, const Q8& q, hipStream_t s, int tile = -1) {
+  if (!h->int8 || !q.w) return gemm(h, pc, a, epi, s, tile);
+  if (a.M > h->aq_rows || (long)a.K > (h->cfg.ffn > h->cfg.hidden ? h->cfg.ffn : h->cfg.hidden))
+    return hipErrorInvalidValue;  // reserve_q8 sizes the rows beforehand
+  int8_t* aq = P<int8_t>(h->aq);
+  float* sx = P<float>(h->asx);
+  prof_arm(h, PC_QUANT);
+  hipError_t e = quant_rows_bf16(a.A, a.lda, aq, a.K, sx, a.M, a.K, s, a.M_dev);
+  if (e != hipSuccess) return e;
+  GemmArgs b = a;
+  b.A = reinterpret_cast<const uint16_t*>(aq); b.lda = a.K;   // bytes
+  b.B = reinterpret_cast<const uint16_t*>(q.w); b.ldb = a.K;
+  b.sx = sx; b.sw = q.s;
+  const int epi8 = epi == EPI_BIAS ? EPI_DQ : epi == EPI_GELU ? EPI_DQ_GELU : epi == EPI_GATE_RES ? EPI_DQ_GATE_RES
+                 : epi == EPI_QKV ? EPI_DQ_QKV : -1;
+  if (epi8 < 0) return hipErrorInvalidValue;
+  prof_arm(h, pc);
+  if (h->ksplit) {
+    b.ws = P<float>(h->splitws);
+    b.ws_elems = (long)(h->splitws.bytes / 4);
+  }
+  return gemm_i8(b, epi8, s, tile);
 }
 
 // Tile shape per GEMM role (indices of gemm_bf16's configurations), chosen from
@@ -202,7 +257,7 @@ int reserve_rows(DfhHandle* h, long M, hipStream_t s) {
     DFH_CHECK(dev_alloc(h->splitws, ((size_t)4096 + (size_t)cus * 256 * 256) * 4));
   }
   h->cap_M = M;
-  return 0;
+  return reserve_q8(h, M, s);
 }
 
 int reserve(DfhHandle* h, int n, int T, int S, hipStream_t s) {
@@ -245,7 +300,7 @@ int reserve(DfhHandle* h, int n, int T, int S, hipStream_t s) {
   h->cap_T = TT;
   h->cap_S = SS;
   h->ld_vt = ld_vt;
-  return 0;
+  return reserve_q8(h, RS > (long)SS * nn ? RS : (long)SS * nn, s);
 }
 
 // c-vector pipeline: timestep rows tv[0..R) (device floats, t then dt), condition
@@ -262,25 +317,25 @@ int build_modulation(DfhHandle* h, int S, int N, bool per_request_t, const float
   DFH_CHECK(gemm(h, PC_OTHER, linear_args(P<uint16_t>(h->temb_in), fd, h->t_w0, h->t_b0,
                                           P<uint16_t>(h->t_hid), H, R, nullptr, H, fd), EPI_BIAS, s));
   DFH_CHECK(silu_bf16(P<uint16_t>(h->t_hid), P<uint16_t>(h->t_hid), (long)R * H, s));
-  DFH_CHECK(gemm(h, PC_OTHER, linear_args(P<uint16_t>(h->t_hid), H, h->t_w2, h->t_b2,
-                                          P<uint16_t>(h->t_out), H, R, nullptr, H, H), EPI_BIAS, s));
+  DFH_CHECK(lin(h, PC_OTHER, linear_args(P<uint16_t>(h->t_hid), H, h->t_w2, h->t_b2,
+                                         P<uint16_t>(h->t_out), H, R, nullptr, H, H), EPI_BIAS, h->t2_q, s));
   const uint16_t* demb = nullptr;
   if (c.meanflow && has_dt) {
     DFH_CHECK(timestep_embed(dt_dev, dt_host, R, freqs, fd / 2, fd, P<uint16_t>(h->temb_in), s));
     DFH_CHECK(gemm(h, PC_OTHER, linear_args(P<uint16_t>(h->temb_in), fd, h->d_w0, h->d_b0,
                                             P<uint16_t>(h->d_hid), H, R, nullptr, H, fd), EPI_BIAS, s));
     DFH_CHECK(silu_bf16(P<uint16_t>(h->d_hid), P<uint16_t>(h->d_hid), (long)R * H, s));
-    DFH_CHECK(gemm(h, PC_OTHER, linear_args(P<uint16_t>(h->d_hid), H, h->d_w2, h->d_b2,
-                                            P<uint16_t>(h->d_out), H, R, nullptr, H, H), EPI_BIAS, s));
+    DFH_CHECK(lin(h, PC_OTHER, linear_args(P<uint16_t>(h->d_hid), H, h->d_w2, h->d_b2,
+                                           P<uint16_t>(h->d_out), H, R, nullptr, H, H), EPI_BIAS, h->d2_q, s));
     demb = P<uint16_t>(h->d_out);
   }
   DFH_CHECK(condition(P<uint16_t>(h->t_out), demb, g, per_request_t ? 1 : S, N, H,
                       P<uint16_t>(h->cond), P<uint16_t>(h->cond_act), s, per_request_t));
   // every block's adaLN (and the final layer's) in one GEMM: [S*N, H] x [ld_mod, H]^T
-  DFH_CHECK(gemm(h, PC_OTHER, linear_args(P<uint16_t>(h->cond_act), H, h->ada_w, h->ada_b,
-                                          P<uint16_t>(h->mod), h->ld_mod,
-                                          (per_request_t ? 1 : S) * N, nullptr, h->ld_mod, H),
-                 EPI_BIAS, s));
+  DFH_CHECK(lin(h, PC_OTHER, linear_args(P<uint16_t>(h->cond_act), H, h->ada_w, h->ada_b,
+                                         P<uint16_t>(h->mod), h->ld_mod,
+                                         (per_request_t ? 1 : S) * N, nullptr, h->ld_mod, H),
+                EPI_BIAS, h->ada_q, s));
   return 0;
 }
 
@@ -339,7 +394,7 @@ int run_latent_tail(DfhHandle* h, const Pass& p, int l, const uint16_t* ml, long
   GemmArgs qa = q_args;
   qa.A = al; qa.lda = H; qa.B = h->qkv_w[l]; qa.ldb = H; qa.N = H; qa.col0 = 0;
   qa.M = NT; qa.M_dev = nullptr; qa.row_pos = p.tail_pos; qa.c_rows = p.tail_rows;
-  DFH_CHECK(gemm(h, PC_TAIL, qa, EPI_QKV, s));
+  DFH_CHECK(lin(h, PC_TAIL, qa, EPI_QKV, h->int8 ? h->qkv_q[l] : Q8{}, s));
   DFH_CHECK(gather_rows(xin, p.tail_rows, nullptr, NT, H, xl, s));  // the block's input rows
   prof_arm(h, PC_TAIL);
   DFH_CHECK(attention_worklist(p.tail_seqs, p.n_seq, h->attq.p, s));
@@ -350,15 +405,15 @@ int run_latent_tail(DfhHandle* h, const Pass& p, int l, const uint16_t* ml, long
                           q_args.rope_q_in_attn ? q_args.rope_sin : nullptr, s));
   GemmArgs o = linear_args(al, H, h->o_w[l], h->o_b[l], xl, H, NT, nullptr, H, H);
   o.gate = ml + 2 * H; o.ld_gate = ldm; o.row_req = p.tail_req;
-  DFH_CHECK(gemm(h, PC_TAIL, o, EPI_GATE_RES, s));
+  DFH_CHECK(lin(h, PC_TAIL, o, EPI_GATE_RES, h->int8 ? h->o_q[l] : Q8{}, s));
   prof_arm(h, PC_TAIL);
   DFH_CHECK(ln_modulate(xl, H, hl, H, ml + 3 * H, ml + 4 * H, ldm, p.tail_req, nullptr, NT, nullptr, H,
                         c.ln_eps, s));
-  DFH_CHECK(gemm(h, PC_TAIL, linear_args(hl, H, h->fc1_w[l], h->fc1_b[l], P<uint16_t>(h->ff), F, NT, nullptr,
-                                         F, H), EPI_GELU, s));
+  DFH_CHECK(lin(h, PC_TAIL, linear_args(hl, H, h->fc1_w[l], h->fc1_b[l], P<uint16_t>(h->ff), F, NT, nullptr,
+                                        F, H), EPI_GELU, h->int8 ? h->fc1_q[l] : Q8{}, s));
   GemmArgs f2 = linear_args(P<uint16_t>(h->ff), F, h->fc2_w[l], h->fc2_b[l], xl, H, NT, nullptr, H, F);
   f2.gate = ml + 5 * H; f2.ld_gate = ldm; f2.row_req = p.tail_req;
-  DFH_CHECK(gemm(h, PC_TAIL, f2, EPI_GATE_RES, s));
+  DFH_CHECK(lin(h, PC_TAIL, f2, EPI_GATE_RES, h->int8 ? h->fc2_q[l] : Q8{}, s));
   return 0;
 }
 
@@ -375,9 +430,9 @@ int run_blocks(DfhHandle* h, const Pass& p, hipStream_t s) {
   if (!p.decode) DFH_CHECK(attention_worklist(p.seqs, p.n_seq, h->attq.p, s));
   // input_layer
   if (!p.x0)
-    DFH_CHECK(gemm(h, PC_OTHER, linear_args(P<uint16_t>(h->seq), H, h->in_w, h->in_b,
-                                            P<uint16_t>(h->x), H, Mup, Md, H, H), EPI_BIAS, s,
-                   tile_for(Mup, H, H, kRoleNarrow)));
+    DFH_CHECK(lin(h, PC_OTHER, linear_args(P<uint16_t>(h->seq), H, h->in_w, h->in_b,
+                                           P<uint16_t>(h->x), H, Mup, Md, H, H), EPI_BIAS, h->in_q, s,
+                  tile_for(Mup, H, H, kRoleNarrow)));
   for (int l = 0; l < c.n_blocks; ++l) {
     const uint16_t* ml = mod + (long)l * 6 * H;  // shift_a, scale_a, gate_a, shift_f, scale_f, gate_f
     // block 0 of a pass with hoisted input rows reads them; its first gate-residual writes h->x
@@ -405,11 +460,13 @@ int run_blocks(DfhHandle* h, const Pass& p, hipStream_t s) {
       // (a prefix pass stops there; a latent tail projects the latent rows' Q)
       GemmArgs kv = q;
       kv.B = h->qkv_w[l] + (long)H * H; kv.N = 2 * H; kv.col0 = H;
-      DFH_CHECK(gemm(h, p.kv_only_last ? PC_QKV : PC_TAIL, kv, EPI_QKV, s, tile_for(Mup, 2 * H, H, kRoleQKV)));
+      Q8 kv8 = h->int8 ? h->qkv_q[l] : Q8{};
+      if (kv8.w) kv8.w += (long)H * H;  // scales stay indexed by the q|k|v column
+      DFH_CHECK(lin(h, p.kv_only_last ? PC_QKV : PC_TAIL, kv, EPI_QKV, kv8, s, tile_for(Mup, 2 * H, H, kRoleQKV)));
       if (p.kv_only_last) break;
       return run_latent_tail(h, p, l, ml, ldm, q, xin, s);
     }
-    DFH_CHECK(gemm(h, PC_QKV, q, EPI_QKV, s, tile_for(Mup, 3 * H, H, kRoleQKV)));
+    DFH_CHECK(lin(h, PC_QKV, q, EPI_QKV, h->int8 ? h->qkv_q[l] : Q8{}, s, tile_for(Mup, 3 * H, H, kRoleQKV)));
     prof_arm(h, PC_ATTN);
     if (p.decode)
       DFH_CHECK(decode_attention(p.qk[l], p.ldqk, p.vt[l], p.ld_vt, P<uint16_t>(h->attn), H, p.seqs, p.n_seq,
@@ -421,17 +478,17 @@ int run_blocks(DfhHandle* h, const Pass& p, hipStream_t s) {
                              Mup, Md, H, H);
     o.gate = ml + 2 * H; o.ld_gate = ldm; o.row_req = row_req;
     if (xin != P<uint16_t>(h->x)) { o.res = xin; o.ld_res = H; }
-    DFH_CHECK(gemm(h, PC_O, o, EPI_GATE_RES, s, tile_for(Mup, H, H, kRoleNarrow)));
+    DFH_CHECK(lin(h, PC_O, o, EPI_GATE_RES, h->int8 ? h->o_q[l] : Q8{}, s, tile_for(Mup, H, H, kRoleNarrow)));
     prof_arm(h, PC_LN);
     DFH_CHECK(ln_modulate(P<uint16_t>(h->x), H, P<uint16_t>(h->hbuf), H, ml + 3 * H, ml + 4 * H, ldm,
                           row_req, nullptr, Mup, Md, H, c.ln_eps, s));
-    DFH_CHECK(gemm(h, PC_FC1, linear_args(P<uint16_t>(h->hbuf), H, h->fc1_w[l], h->fc1_b[l],
-                                          P<uint16_t>(h->ff), F, Mup, Md, F, H), EPI_GELU, s,
-                   tile_for(Mup, F, H, kRoleWide)));
+    DFH_CHECK(lin(h, PC_FC1, linear_args(P<uint16_t>(h->hbuf), H, h->fc1_w[l], h->fc1_b[l],
+                                         P<uint16_t>(h->ff), F, Mup, Md, F, H), EPI_GELU,
+                  h->int8 ? h->fc1_q[l] : Q8{}, s, tile_for(Mup, F, H, kRoleWide)));
     GemmArgs f2 = linear_args(P<uint16_t>(h->ff), F, h->fc2_w[l], h->fc2_b[l], P<uint16_t>(h->x), H,
                               Mup, Md, H, F);
     f2.gate = ml + 5 * H; f2.ld_gate = ldm; f2.row_req = row_req;
-    DFH_CHECK(gemm(h, PC_FC2, f2, EPI_GATE_RES, s, tile_for(Mup, H, F, kRoleNarrow)));
+    DFH_CHECK(lin(h, PC_FC2, f2, EPI_GATE_RES, h->int8 ? h->fc2_q[l] : Q8{}, s, tile_for(Mup, H, F, kRoleNarrow)));
   }
   return 0;
 }
@@ -501,15 +558,15 @@ int solve_steps(DfhHandle* h, int n, int T, int S, const void* g_cond, const voi
   const int NP = n * Pp;
   // input_layer of every packed row once: a history row's does not depend on the
   // step (no t or z); the latent rows' are replaced every step
-  DFH_CHECK(gemm(h, PC_OTHER, linear_args(P<uint16_t>(h->seq), H, h->in_w, h->in_b, P<uint16_t>(h->x0), H,
-                                          n * T, P<int>(h->counts), H, H), EPI_BIAS, s,
-                 tile_for(n * T, H, H, kRoleNarrow)));
+  DFH_CHECK(lin(h, PC_OTHER, linear_args(P<uint16_t>(h->seq), H, h->in_w, h->in_b, P<uint16_t>(h->x0), H,
+                                         n * T, P<int>(h->counts), H, H), EPI_BIAS, h->in_q, s,
+                tile_for(n * T, H, H, kRoleNarrow)));
   for (int st = 0; st < S; ++st) {
     // zp = coordinate_proj(z); its input_layer rows -> the latent rows of x0
     DFH_CHECK(gemm(h, PC_OTHER, linear_args(P<uint16_t>(h->z), ld, h->coord_w, h->coord_b,
                                             P<uint16_t>(h->zp), H, NP, nullptr, H, ld), EPI_BIAS, s));
-    DFH_CHECK(gemm(h, PC_OTHER, linear_args(P<uint16_t>(h->zp), H, h->in_w, h->in_b, P<uint16_t>(h->fin), H,
-                                            NP, nullptr, H, H), EPI_BIAS, s));
+    DFH_CHECK(lin(h, PC_OTHER, linear_args(P<uint16_t>(h->zp), H, h->in_w, h->in_b, P<uint16_t>(h->fin), H,
+                                           NP, nullptr, H, H), EPI_BIAS, h->in_q, s));
     DFH_CHECK(scatter_rows(P<uint16_t>(h->fin), P<int>(h->patch_rows), NP, H, P<uint16_t>(h->x0), s));
     const bool tail = h->latent_tail;
     if (dit_blocks(h, n, T, (long)st * n, s, tail, P<uint16_t>(h->x0))) return 1;
@@ -566,7 +623,7 @@ int dfh_destroy(DfhHandle* h) {
                     &h->hist_len, &h->counts, &h->err, &h->patch_rows, &h->seqs, &h->rope_cos, &h->rope_sin,
                     &h->temb_in, &h->t_hid, &h->t_out, &h->d_hid, &h->d_out, &h->cond,
                     &h->cond_act, &h->mod, &h->z, &h->zp, &h->fin, &h->vel, &h->tvals, &h->splitws, &h->attq,
-                    &h->x0, &h->tail_seqs, &h->tail_req, &h->tail_pos};
+                    &h->x0, &h->tail_seqs, &h->tail_req, &h->tail_pos, &h->w8, &h->aq, &h->asx};
   for (DevBuf* b : bufs)
     if (b->p) (void)hipFree(b->p);
   for (hipEvent_t ev : h->ev_pool) (void)hipEventDestroy(ev);
@@ -575,6 +632,7 @@ int dfh_destroy(DfhHandle* h) {
 }
 
 int dfh_set_weights(DfhHandle* h, const DfhWeights* w, void* stream) {
+  if (h) h->int8 = false;  // the int8 weights were made from the previous weights
   if (!h || !w || !w->blocks) return fail("null argument");
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const DfhConfig& c = h->cfg;
@@ -682,6 +740,74 @@ int dfh_set_weights(DfhHandle* h, const DfhWeights* w, void* stream) {
     h->kn_w[l] = at(o_kn_w[l]); h->kn_b[l] = at(o_kn_b[l]);
   }
   h->weights_set = true;
+  return 0;
+}
+
+// W8A8 mode of the solve and forward (the reference's quantize_dit_ on the DiT,
+// int8_dit.py:34-85): the int8 weights come from the caller or are quantised
+// here from the handle's bf16 weights, as Int8DynamicLinear(lin) does.
+int dfh_set_int8(DfhHandle* h, int enable, const DfhInt8Weights* w, void* stream) {
+  if (!h) return fail("dfh_set_int8: NULL handle");
+  if (!enable) {
+    h->int8 = false;
+    return 0;
+  }
+  if (!h->weights_set) return fail("dfh_set_int8: set the weights first");
+  const DfhConfig& c = h->cfg;
+  const long H = c.hidden, F = c.ffn;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  struct Item {
+    const uint16_t* src;      // bf16 [N, K]
+    DfhInt8Linear given;      // caller's int8 weight (NULL: quantise src)
+    long N, K;
+    Q8* dst;
+  };
+  std::vector<Item> items;
+  auto given = [&](const DfhInt8Linear* a) { return a ? *a : DfhInt8Linear{nullptr, nullptr}; };
+  h->qkv_q.assign(c.n_blocks, Q8{});
+  h->o_q.assign(c.n_blocks, Q8{});
+  h->fc1_q.assign(c.n_blocks, Q8{});
+  h->fc2_q.assign(c.n_blocks, Q8{});
+  h->d2_q = Q8{};
+  items.push_back({h->in_w, given(w ? &w->input : nullptr), H, H, &h->in_q});
+  items.push_back({h->t_w2, given(w ? &w->t_mlp2 : nullptr), H, H, &h->t2_q});
+  if (c.meanflow) items.push_back({h->d_w2, given(w ? &w->d_mlp2 : nullptr), H, H, &h->d2_q});
+  items.push_back({h->ada_w, given(w ? &w->ada : nullptr), h->ld_mod, H, &h->ada_q});
+  for (int l = 0; l < c.n_blocks; ++l) {
+    items.push_back({h->qkv_w[l], given(w && w->qkv ? &w->qkv[l] : nullptr), 3 * H, H, &h->qkv_q[l]});
+    items.push_back({h->o_w[l], given(w && w->o ? &w->o[l] : nullptr), H, H, &h->o_q[l]});
+    items.push_back({h->fc1_w[l], given(w && w->fc1 ? &w->fc1[l] : nullptr), F, H, &h->fc1_q[l]});
+    items.push_back({h->fc2_w[l], given(w && w->fc2 ? &w->fc2[l] : nullptr), H, F, &h->fc2_q[l]});
+  }
+  long total = 0;
+  std::vector<long> wo, so;
+  for (auto& it : items) {
+    if ((it.given.w == nullptr) != (it.given.scale == nullptr))
+      return fail("dfh_set_int8: an int8 weight needs both its values and its scales");
+    wo.push_back(total);
+    total = (total + it.N * it.K + 255) / 256 * 256;
+    so.push_back(total);
+    total = (total + it.N * 4 + 255) / 256 * 256;
+  }
+  DFH_CHECK(hipStreamSynchronize(s));
+  h->int8 = false;
+  DFH_CHECK(dev_alloc(h->w8, total));
+  for (size_t i = 0; i < items.size(); ++i) {
+    Item& it = items[i];
+    int8_t* q = P<int8_t>(h->w8) + wo[i];
+    float* sc = reinterpret_cast<float*>(P<char>(h->w8) + so[i]);
+    if (it.given.w) {
+      DFH_CHECK(hipMemcpyAsync(q, it.given.w, it.N * it.K, hipMemcpyDeviceToDevice, s));
+      DFH_CHECK(hipMemcpyAsync(sc, it.given.scale, it.N * 4, hipMemcpyDeviceToDevice, s));
+    } else {
+      DFH_CHECK(quant_weight_f32(it.src, q, sc, (int)it.N, (int)it.K, s));
+    }
+    *it.dst = Q8{q, sc};
+  }
+  h->int8 = true;
+  const long rows = h->cap_M > (long)h->cap_S * h->cap_n ? h->cap_M : (long)h->cap_S * h->cap_n;
+  if (reserve_q8(h, rows > 0 ? rows : 1, s)) return 1;
+  DFH_CHECK(hipStreamSynchronize(s));
   return 0;
 }
 

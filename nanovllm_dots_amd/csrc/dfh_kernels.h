@@ -25,7 +25,18 @@ enum Epilogue : int {
   EPI_I32 = 5,       // int8 operands: Ci = int32 accumulators
   EPI_DQ = 6,        // int8 operands: C = bf16(((float(acc) * sx[m]) * sw[n]) + bias[n])
   EPI_SILU = 7,      // C = bf16(silu(bf16(acc + bias)))
+  // int8 operands, the linear's output dequantised first, y = ((float(acc) * sx[m]) * sw[n]) + bias[n]
+  // (int8_dit.py:60-63), then the bf16 epilogue of the same name on bf16(y)
+  EPI_DQ_GELU = 8,
+  EPI_DQ_GATE_RES = 9,
+  EPI_DQ_QKV = 10,
 };
+// the dequantising epilogues and the bf16 epilogue each continues with
+constexpr bool is_dq(int e) { return e == EPI_DQ || e == EPI_DQ_GELU || e == EPI_DQ_GATE_RES || e == EPI_DQ_QKV; }
+constexpr int base_epi(int e) {
+  return e == EPI_DQ ? EPI_BIAS : e == EPI_DQ_GELU ? EPI_GELU : e == EPI_DQ_GATE_RES ? EPI_GATE_RES
+       : e == EPI_DQ_QKV ? EPI_QKV : e;
+}
 
 struct GemmArgs {
   const uint16_t* A; long lda;       // [M, K] bf16 activations, K contiguous
@@ -71,7 +82,7 @@ hipError_t gemm_i8(const GemmArgs& a, int epi, hipStream_t s, int tile_hint = -1
 // Per-row dynamic int8 quantisation of a bf16 [M, K] matrix (Int8DynamicLinear,
 // int8_dit.py:57-58): s = max(bf16(amax/127), bf16(1e-8)); q = clamp(rint(bf16(x/s)), +-127).
 hipError_t quant_rows_bf16(const uint16_t* x, long ldx, int8_t* q, long ldq, float* scale, int M, int K,
-                           hipStream_t s);
+                           hipStream_t s, const int* M_dev = nullptr);  // M_dev: device row count (M: bound)
 // Per-output-channel int8 weight quantisation in float32 (int8_dit.py:40-45).
 hipError_t quant_weight_f32(const uint16_t* w, int8_t* q, float* scale, int N, int K, hipStream_t s);
 

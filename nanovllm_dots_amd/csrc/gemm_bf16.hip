@@ -136,14 +136,15 @@ struct OpI8 {
 // 16 B per lane, one 32-row block ahead of the block it stores.
 template <class C, int EPI>
 struct Staged {
-  static constexpr bool kEpi = EPI == EPI_BIAS || EPI == EPI_GELU || EPI == EPI_SILU || EPI == EPI_GATE_RES;
+  static constexpr int B = base_epi(EPI);
+  static constexpr bool kEpi = B == EPI_BIAS || B == EPI_GELU || B == EPI_SILU || B == EPI_GATE_RES;
   static constexpr int kSmall = C::BM < C::BN ? C::BM : C::BN;
   static constexpr bool value = kEpi && (C::NW / 2) * 32 * C::WTN <= kSmall * C::BK && C::NW % 2 == 0;
   static constexpr int CPR = C::WTN / 8;   // 16-B chunks per staged row
   static constexpr int RPI = 64 / CPR;     // rows per wave-wide 16-B access
   static constexpr int JB = 32 / RPI;      // wave-wide accesses per 32-row block
   static constexpr int kStores = C::RM * JB;
-  static constexpr bool kRes = EPI == EPI_GATE_RES;
+  static constexpr bool kRes = B == EPI_GATE_RES;
   // vector-memory ops the epilogue issues after the next tile's prologue DMA
   // (stores, and the residual + gate loads of blocks 1 .. RM-1), on every path
   static constexpr int kVmAfter = kStores + (kRes ? (C::RM - 1) * 2 * JB : 0);
@@ -162,8 +163,8 @@ template <class C, int EPI>
 struct StagedOperands {
   static constexpr int JB = Staged<C, EPI>::JB, NRES = Staged<C, EPI>::kRes ? JB : 1;
   float b[C::RN][4][4];
-  float w[EPI == EPI_DQ ? C::RN : 1][4][4];
-  float sx[EPI == EPI_DQ ? C::RM : 1];
+  float w[is_dq(EPI) ? C::RN : 1][4][4];
+  float sx[is_dq(EPI) ? C::RM : 1];
   uint4 x0[NRES], g0[NRES];  // gate-residual: residual and gate chunks of block 0
 };
 
@@ -228,12 +229,12 @@ __device__ __forceinline__ void staged_preload(const GemmArgs& a, StagedOperands
     for (int g = 0; g < 4; ++g) {
       const int n = n0 + wn * C::WTN + i * 32 + 8 * g + 4 * hi;
       unpack4(braw[i][g], op.b[i][g]);
-      if constexpr (EPI == EPI_DQ) {
+      if constexpr (is_dq(EPI)) {
         const float4 w4 = *reinterpret_cast<const float4*>(a.sw + n);
         op.w[i][g][0] = w4.x; op.w[i][g][1] = w4.y; op.w[i][g][2] = w4.z; op.w[i][g][3] = w4.w;
       }
     }
-  if constexpr (EPI == EPI_DQ) {
+  if constexpr (is_dq(EPI)) {
 #pragma unroll
     for (int k = 0; k < C::RM; ++k) {
       const int m = m0 + wm * C::WTM + k * 32 + l32;
@@ -267,7 +268,7 @@ __device__ __forceinline__ void staged_epilogue(const GemmArgs& a, ACC (&acc)[C:
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         float y[4];
-        if constexpr (EPI == EPI_DQ) {
+        if constexpr (is_dq(EPI)) {
           // ((acc.f32 * s_x) * s_w) + bias, each op rounded to float32 (int8_dit.py:60-62)
 #pragma unroll
           for (int t = 0; t < 4; ++t)
@@ -276,10 +277,10 @@ __device__ __forceinline__ void staged_epilogue(const GemmArgs& a, ACC (&acc)[C:
 #pragma unroll
           for (int t = 0; t < 4; ++t) y[t] = acc[i][k][4 * g + t] + op.b[i][g][t];
         }
-        if constexpr (EPI == EPI_GELU) {
+        if constexpr (base_epi(EPI) == EPI_GELU) {
 #pragma unroll
           for (int t = 0; t < 4; ++t) y[t] = gelu_tanh_f(rbf(y[t]));
-        } else if constexpr (EPI == EPI_SILU) {
+        } else if constexpr (base_epi(EPI) == EPI_SILU) {
 #pragma unroll
           for (int t = 0; t < 4; ++t) y[t] = silu_fast(rbf(y[t]));
         }
@@ -324,10 +325,16 @@ __device__ __forceinline__ void staged_epilogue(const GemmArgs& a, ACC (&acc)[C:
 // q / k: bias, optional per-head LayerNorm / RMSNorm over 64, RoPE on the
 // column pairs (d, d+32) that a lane holds in blocks (i, i+1); v: transposed
 // into V^T[column][vt_col[row]].
-template <class C, class ACC>
+template <class C, bool DQ, class ACC>
 __device__ __forceinline__ void qkv_epilogue(const GemmArgs& a, ACC (&acc)[C::RN][C::RM], int m0, int n0,
                                              int M, int wm, int wn, int l32, int hi) {
   const int H = a.hidden;
+  // the linear's output of accumulator e, output column n (within q|k|v), bias b:
+  // acc + b, or with int8 operands ((acc * s_x) * s_w) + b (int8_dit.py:60-62)
+  auto lin = [&](auto e, float sxm, int n, float b) {
+    if constexpr (DQ) return add_rn(mul_rn(mul_rn((float)e, sxm), a.sw[n]), b);
+    else return (float)e + b;
+  };
   n0 += a.col0;               // column within the fused q|k|v output
   const int region = n0 / H;  // 0 q, 1 k, 2 v (BN divides H)
 #pragma unroll
@@ -335,6 +342,7 @@ __device__ __forceinline__ void qkv_epilogue(const GemmArgs& a, ACC (&acc)[C::RN
     const int m = m0 + wm * C::WTM + k * 32 + l32;
     const bool valid = m < M;
     const int mm = valid ? m : M - 1;
+    const float sxm = DQ ? a.sx[mm] : 0.f;
     if (region == 2) {
       const int col = a.vt_col[mm];
 #pragma unroll
@@ -343,7 +351,7 @@ __device__ __forceinline__ void qkv_epilogue(const GemmArgs& a, ACC (&acc)[C::RN
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
           const int n = nb + 8 * (v >> 2) + 4 * hi + (v & 3);
-          float y = acc[i][k][v] + (a.bias ? bf2f(a.bias[n + 2 * H]) : 0.f);
+          float y = lin(acc[i][k][v], sxm, n + 2 * H, a.bias ? bf2f(a.bias[n + 2 * H]) : 0.f);
           if (valid) a.vt[(long)n * a.ld_vt + col] = f2bf(y);
         }
       }
@@ -362,8 +370,8 @@ __device__ __forceinline__ void qkv_epilogue(const GemmArgs& a, ACC (&acc)[C::RN
         const int d = 8 * (v >> 2) + 4 * hi + (v & 3);
         float b0 = a.bias ? bf2f(a.bias[nb + d]) : 0.f;
         float b1 = a.bias ? bf2f(a.bias[nb + 32 + d]) : 0.f;
-        x0[v] = rbf(acc[i][k][v] + b0);
-        x1[v] = rbf(acc[i + 1][k][v] + b1);
+        x0[v] = rbf(lin(acc[i][k][v], sxm, nb + d, b0));
+        x1[v] = rbf(lin(acc[i + 1][k][v], sxm, nb + 32 + d, b1));
       }
       if (a.qk_norm) {
         float s = 0.f, s2 = 0.f;
@@ -420,8 +428,8 @@ __device__ __forceinline__ void qkv_epilogue(const GemmArgs& a, ACC (&acc)[C::RN
 template <class C, int EPI, class ACC>
 __device__ __forceinline__ void run_epilogue(const GemmArgs& a, ACC (&acc)[C::RN][C::RM], int m0,
                                              int n0, int M, int wm, int wn, int l32, int hi) {
-    if constexpr (EPI == EPI_QKV) {
-      qkv_epilogue<C>(a, acc, m0, n0, M, wm, wn, l32, hi);
+    if constexpr (base_epi(EPI) == EPI_QKV) {
+      qkv_epilogue<C, is_dq(EPI)>(a, acc, m0, n0, M, wm, wn, l32, hi);
     } else {
       // bias (and int8 weight scale) of this lane's output columns, hoisted out of
       // the row loop for narrow wave tiles (wide ones reload them: registers)
@@ -443,7 +451,7 @@ __device__ __forceinline__ void run_epilogue(const GemmArgs& a, ACC (&acc)[C::RN
         for (int g = 0; g < 4; ++g) {
           const int n = n0 + wn * C::WTN + i * 32 + 8 * g + 4 * hi_;
           unpack4(braw[g], b4[g]);
-          if constexpr (EPI == EPI_DQ) {
+          if constexpr (is_dq(EPI)) {
             const float4 q4 = *reinterpret_cast<const float4*>(a.sw + n);
             w4[g][0] = q4.x; w4[g][1] = q4.y; w4[g][2] = q4.z; w4[g][3] = q4.w;
           }
@@ -471,9 +479,9 @@ __device__ __forceinline__ void run_epilogue(const GemmArgs& a, ACC (&acc)[C::RN
         const uint32_t rowoff = (uint32_t)r * (uint32_t)a.ldc;
         const uint16_t* xrow = a.res ? a.res + (long)mm * a.ld_res : a.C + (long)mm * a.ldc;
         const uint16_t* grow = nullptr;
-        if constexpr (EPI == EPI_GATE_RES) grow = a.gate + (long)a.row_req[mm] * a.ld_gate;
+        if constexpr (base_epi(EPI) == EPI_GATE_RES) grow = a.gate + (long)a.row_req[mm] * a.ld_gate;
         float sxm = 0.f;
-        if constexpr (EPI == EPI_DQ) sxm = a.sx[mm];
+        if constexpr (is_dq(EPI)) sxm = a.sx[mm];
 #pragma unroll
         for (int i = 0; i < C::RN; ++i) {
           const int nb = n0 + wn * C::WTN + i * 32 + 4 * hi;
@@ -490,7 +498,7 @@ __device__ __forceinline__ void run_epilogue(const GemmArgs& a, ACC (&acc)[C::RN
                                (uint32_t)acc[i][k][4 * g + 2], (uint32_t)acc[i][k][4 * g + 3]};
               __builtin_amdgcn_raw_buffer_store_b128(v, rc, off, 0, 0);
               continue;
-            } else if constexpr (EPI == EPI_DQ) {
+            } else if constexpr (is_dq(EPI)) {
               // ((acc.f32 * s_x) * s_w) + bias, each op rounded to float32 (int8_dit.py:60-62)
 #pragma unroll
               for (int t = 0; t < 4; ++t)
@@ -504,13 +512,13 @@ __device__ __forceinline__ void run_epilogue(const GemmArgs& a, ACC (&acc)[C::RN
                                __float_as_uint(y[3])};
               __builtin_amdgcn_raw_buffer_store_b128(v, rc, off, 0, 0);
               continue;
-            } else if constexpr (EPI == EPI_GELU) {
+            } else if constexpr (base_epi(EPI) == EPI_GELU) {
 #pragma unroll
               for (int t = 0; t < 4; ++t) y[t] = gelu_tanh_f(rbf(y[t]));
-            } else if constexpr (EPI == EPI_SILU) {
+            } else if constexpr (base_epi(EPI) == EPI_SILU) {
 #pragma unroll
               for (int t = 0; t < 4; ++t) y[t] = silu_fast(rbf(y[t]));
-            } else if constexpr (EPI == EPI_GATE_RES) {
+            } else if constexpr (base_epi(EPI) == EPI_GATE_RES) {
               float gt[4], xr[4];
               unpack4(*reinterpret_cast<const uint2*>(grow + n), gt);
               unpack4(*reinterpret_cast<const uint2*>(xrow + n), xr);
@@ -710,7 +718,7 @@ gemm_mfma_kernel(GemmArgs a) {
   // tile's first step waits for vmcnt <= kEpiStores (+ the later prologue
   // stages) and leaves the stores in flight. The QKV epilogue (data-dependent
   // store count) waits for zero.
-  constexpr int kEpiStoresRaw = (EPI == EPI_QKV) ? -1 : Staged<C, EPI>::value ? Staged<C, EPI>::kVmAfter
+  constexpr int kEpiStoresRaw = (base_epi(EPI) == EPI_QKV) ? -1 : Staged<C, EPI>::value ? Staged<C, EPI>::kVmAfter
                                                                              : C::RN * C::RM * 4;
   constexpr int kWaitBase = ST >= 2 ? (ST - 2) * C::LPS : 0;
   // vmcnt holds at most 63: larger counts fall back to a full wait
@@ -761,7 +769,7 @@ gemm_mfma_kernel(GemmArgs a) {
   // vector-memory ops a staged epilogue issues after the next tile's prologue
   // (stores, residual / gate loads) plus the row -> request loads of the next
   // tile's start; -1: unknown or too many to count (then those waits drain fully)
-  constexpr int kVm2Raw = (EPI == EPI_QKV || !Staged<C, EPI>::value)
+  constexpr int kVm2Raw = (base_epi(EPI) == EPI_QKV || !Staged<C, EPI>::value)
                               ? -1
                               : Staged<C, EPI>::kVmAfter + (Staged<C, EPI>::kRes ? C::RM * Staged<C, EPI>::JB : 0);
   constexpr int kVm2 = kVm2Raw > 63 ? 63 : kVm2Raw;
@@ -1196,11 +1204,17 @@ hipError_t gemm_i8(const GemmArgs& a_bytes, int epi, hipStream_t s, int tile) {
   a.ldb = a_bytes.ldb / 2;
   if (tile < 0) tile = pick_tile(a);
   if (tile < 0 || tile >= kNumTiles) return hipErrorInvalidValue;
+  if (epi == EPI_DQ_QKV && kTileWTN[tile] < 64) tile = 2;  // RoPE pairs need a 64-column wave tile
   if (a.N % kTileBN[tile] != 0 || a.K % kTileBK[tile] != 0) return hipErrorInvalidValue;
+  if (epi == EPI_DQ_QKV && (a.hidden % kTileBN[tile] != 0 || a.head_dim != 64)) return hipErrorInvalidValue;
+  if (is_dq(epi) && (!a.sx || !a.sw)) return hipErrorInvalidValue;
   if ((long)a.M * a.lda >= (1L << 31) || (long)a.N * a.ldb >= (1L << 31)) return hipErrorInvalidValue;
   switch (epi) {
     case EPI_I32: return dispatch_tiles<OpI8, EPI_I32>(a, s, tile);
     case EPI_DQ: return dispatch_tiles<OpI8, EPI_DQ>(a, s, tile);
+    case EPI_DQ_GELU: return dispatch_tiles<OpI8, EPI_DQ_GELU>(a, s, tile);
+    case EPI_DQ_GATE_RES: return dispatch_tiles<OpI8, EPI_DQ_GATE_RES>(a, s, tile);
+    case EPI_DQ_QKV: return dispatch_tiles<OpI8, EPI_DQ_QKV>(a, s, tile);
     default: return hipErrorInvalidValue;
   }
 }

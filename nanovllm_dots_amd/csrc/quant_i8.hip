@@ -24,10 +24,10 @@ namespace {
 template <int NCH>
 __global__ void __launch_bounds__(256)
 quant_rows_kernel(const uint16_t* __restrict__ x, long ldx, int8_t* __restrict__ q, long ldq,
-                  float* __restrict__ scale, int M, int K) {
+                  float* __restrict__ scale, int M, int K, const int* __restrict__ M_dev) {
   const int lane = threadIdx.x & 63;
   const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (r >= M) return;
+  if (r >= (M_dev ? *M_dev : M)) return;
   const uint16_t* xp = x + (long)r * ldx;
   constexpr int NR = NCH > 0 ? NCH : 1;
   uint4 row[NR];
@@ -99,15 +99,23 @@ quant_weight_kernel(const uint16_t* __restrict__ w, int8_t* __restrict__ q, floa
 }  // namespace
 
 hipError_t quant_rows_bf16(const uint16_t* x, long ldx, int8_t* q, long ldq, float* scale, int M, int K,
-                           hipStream_t s) {
+                           hipStream_t s, const int* M_dev) {
   if (M <= 0) return hipSuccess;
   if (K <= 0 || K % 8 != 0 || ldx % 8 != 0 || ldq % 8 != 0) return hipErrorInvalidValue;
   const dim3 grid((M + 3) / 4), block(256);
   switch (K) {
-    case 1024: hipLaunchKernelGGL(quant_rows_kernel<2>, grid, block, 0, s, x, ldx, q, ldq, scale, M, K); break;
-    case 2048: hipLaunchKernelGGL(quant_rows_kernel<4>, grid, block, 0, s, x, ldx, q, ldq, scale, M, K); break;
-    case 4096: hipLaunchKernelGGL(quant_rows_kernel<8>, grid, block, 0, s, x, ldx, q, ldq, scale, M, K); break;
-    default: hipLaunchKernelGGL(quant_rows_kernel<0>, grid, block, 0, s, x, ldx, q, ldq, scale, M, K); break;
+    case 1024:
+      dfh_launch(quant_rows_kernel<2>, grid, block, 0, s, x, ldx, q, ldq, scale, M, K, M_dev);
+      break;
+    case 2048:
+      dfh_launch(quant_rows_kernel<4>, grid, block, 0, s, x, ldx, q, ldq, scale, M, K, M_dev);
+      break;
+    case 4096:
+      dfh_launch(quant_rows_kernel<8>, grid, block, 0, s, x, ldx, q, ldq, scale, M, K, M_dev);
+      break;
+    default:
+      dfh_launch(quant_rows_kernel<0>, grid, block, 0, s, x, ldx, q, ldq, scale, M, K, M_dev);
+      break;
   }
   return hipGetLastError();
 }

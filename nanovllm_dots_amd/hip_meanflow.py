@@ -102,7 +102,7 @@ class HipFMHead:
     """Owns one library handle: packed weights + a growable workspace."""
 
     def __init__(self, spec: FMSpec, weights: dict[str, torch.Tensor], device=None,
-                 inv_freq: torch.Tensor | None = None):
+                 inv_freq: torch.Tensor | None = None, int8: bool = False):
         self.lib = _lib.lib()
         self.spec = spec
         self.device = torch.device(device if device is not None else "cuda")
@@ -122,12 +122,48 @@ class HipFMHead:
         with torch.cuda.device(self.device):
             _lib.check(self.lib.dfh_create(C.byref(cfg), C.byref(h)), "dfh_create")
         self.handle = h
+        self.int8 = False
         self.set_weights(weights)
+        if int8 and not self.int8:
+            self.set_int8(True)
 
     # -- weights --------------------------------------------------------------
+    def int8_linear_names(self) -> list[str]:
+        """The DiT linears quantize_dit_ turns into W8A8 (min(in, out) >= 512,
+        D/int8_dit.py:71-85), in the order the library packs them."""
+        s = self.spec
+        names = ["input_layer", "time_embedder.mlp.2"] + (["duration_embedder.mlp.2"] if s.meanflow else [])
+        for l in range(s.n_blocks):
+            p = f"blocks.{l}."
+            names += [p + n for n in ("attn.q_proj", "attn.k_proj", "attn.v_proj", "attn.o_proj", "ffn.fc1",
+                                      "ffn.fc2", "adaLN_modulation.1")]
+        return names + ["output_layer.adaLN_modulation.1"]
+
+    @staticmethod
+    def _split_int8(W: dict[str, torch.Tensor]):
+        """A quantize_dit_-ed state dict holds, per W8A8 linear, an int8 weight
+        (Int8DynamicLinear: ``Wt_int8`` [in, out]; HipInt8Linear: ``W_int8``
+        [out, in]) and ``w_scale`` instead of ``weight``. Returns the state dict
+        with a bf16 stand-in ``weight`` (q * s, used only if W8A8 is switched
+        off) and {linear: (int8 [out, in], scale [out])}."""
+        W = dict(W)
+        q8 = {}
+        for k in list(W):
+            for suffix, transpose in ((".Wt_int8", True), (".W_int8", False)):
+                if k.endswith(suffix):
+                    name = k[: -len(suffix)]
+                    q = W.pop(k)
+                    q = (q.t() if transpose else q).contiguous()
+                    sc = W.pop(name + ".w_scale").float().contiguous()
+                    q8[name] = (q, sc)
+                    if name + ".weight" not in W:
+                        W[name + ".weight"] = (q.float() * sc[:, None]).to(torch.bfloat16)
+        return W, q8
+
     def set_weights(self, W: dict[str, torch.Tensor]) -> None:
         s = self.spec
         keep = []
+        W, q8 = self._split_int8(W)
 
         def dev(name, required=True):
             t = W.get(name)
@@ -174,6 +210,52 @@ class HipFMHead:
             _lib.check(self.lib.dfh_set_weights(self.handle, C.byref(w), _lib.stream_ptr()),
                        "dfh_set_weights")
         del keep
+        self.int8 = False
+        if q8:
+            self.set_int8(True, q8)
+
+    def set_int8(self, enable: bool, q8: dict | None = None) -> None:
+        """W8A8 solve (the reference's quantize_dit_ DiT, D/int8_dit.py): every
+        linear of int8_linear_names() runs as Int8DynamicLinear. Its int8 weights
+        come from q8 ({linear: (int8 [out, in], scale [out])}, as a quantized
+        module holds them) or, without q8, are quantised from the bf16 weights
+        as Int8DynamicLinear(lin) does. A partly quantised DiT is refused."""
+        if not enable:
+            _lib.check(self.lib.dfh_set_int8(self.handle, 0, None, _lib.stream_ptr()), "dfh_set_int8")
+            self.int8 = False
+            return
+        s = self.spec
+        names = self.int8_linear_names()
+        arg = None
+        keep = []
+        if q8:
+            missing = [n for n in names if n not in q8]
+            if missing:
+                raise RuntimeError(f"partly quantised DiT: no int8 weight for {missing[:4]}")
+
+            def lin(*parts):
+                q = torch.cat([q8[p][0] for p in parts]).to(self.device, torch.int8).contiguous()
+                sc = torch.cat([q8[p][1] for p in parts]).to(self.device, torch.float32).contiguous()
+                keep.extend((q, sc))
+                return _lib.DfhInt8Linear(_lib.ptr(q), _lib.ptr(sc))
+
+            L = s.n_blocks
+            qkv, o, fc1, fc2 = ((_lib.DfhInt8Linear * L)() for _ in range(4))
+            for l in range(L):
+                p = f"blocks.{l}."
+                qkv[l] = lin(p + "attn.q_proj", p + "attn.k_proj", p + "attn.v_proj")
+                o[l], fc1[l], fc2[l] = lin(p + "attn.o_proj"), lin(p + "ffn.fc1"), lin(p + "ffn.fc2")
+            arg = _lib.DfhInt8Weights(
+                input=lin("input_layer"), t_mlp2=lin("time_embedder.mlp.2"),
+                d_mlp2=lin("duration_embedder.mlp.2") if s.meanflow else _lib.DfhInt8Linear(None, None),
+                ada=lin(*[f"blocks.{l}.adaLN_modulation.1" for l in range(L)], "output_layer.adaLN_modulation.1"),
+                qkv=C.cast(qkv, C.POINTER(_lib.DfhInt8Linear)), o=C.cast(o, C.POINTER(_lib.DfhInt8Linear)),
+                fc1=C.cast(fc1, C.POINTER(_lib.DfhInt8Linear)), fc2=C.cast(fc2, C.POINTER(_lib.DfhInt8Linear)))
+        with torch.cuda.device(self.device):
+            _lib.check(self.lib.dfh_set_int8(self.handle, 1, C.byref(arg) if arg is not None else None,
+                                             _lib.stream_ptr()), "dfh_set_int8")
+        del keep
+        self.int8 = True
 
     # -- entry points -----------------------------------------------------------
     def solve(self, input_sequence, pos_ids, g_cond, noise, num_steps: int, *, strict=False):
@@ -287,7 +369,7 @@ class HipFMHead:
         _lib.check(self.lib.dfh_profile_enable(self.handle, int(enable)), "dfh_profile_enable")
 
     PROFILE_CLASSES = ("qkv_gemm", "o_gemm", "fc1_gemm", "fc2_gemm", "attention", "ln_modulate", "other",
-                       "latent_tail")
+                       "latent_tail", "quantise")
 
     def profile_read(self) -> dict[str, tuple[float, int]]:
         k = len(self.PROFILE_CLASSES)

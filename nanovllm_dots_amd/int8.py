@@ -83,14 +83,12 @@ class HipInt8Linear(nn.Module):
 
 
 def quantize_dit_(dit, *, min_features: int = 512) -> int:
-    """Replace eligible nn.Linear in ``dit`` with HipInt8Linear in place (same
-    eligibility rule as int8_dit.py:71-85). Returns the count quantised."""
-    n = 0
-    for _name, mod in dit.named_modules():
-        for child_name, child in list(mod.named_children()):
-            if isinstance(child, nn.Linear) and not isinstance(child, HipInt8Linear):
-                if min(child.in_features, child.out_features) < min_features:
-                    continue
-                setattr(mod, child_name, HipInt8Linear(child))
-                n += 1
-    return n
+    """W8A8 every plain nn.Linear of ``dit`` whose smaller side has at least
+    ``min_features`` features (the eligibility rule of int8_dit.py:71-85), in
+    place; returns how many were replaced. ``HipFMHead`` takes such a module's
+    int8 weights as they are (its W8A8 solve)."""
+    targets = [(parent, name, child) for parent in dit.modules() for name, child in parent.named_children()
+               if type(child) is nn.Linear and min(child.in_features, child.out_features) >= min_features]
+    for parent, name, child in targets:
+        setattr(parent, name, HipInt8Linear(child))
+    return len(targets)

@@ -142,30 +142,56 @@ def round_bf16(t: torch.Tensor) -> torch.Tensor:
 
 
 def weights_for_regime(W: dict[str, torch.Tensor], regime: str) -> dict[str, torch.Tensor]:
-    """bf16 regime: the parameters are bf16 tensors (N/loader.py:58-63)."""
-    if regime == "bf16":
+    """bf16 and int8 regimes: the parameters are bf16 tensors (N/loader.py:58-63)."""
+    if regime in ("bf16", "int8"):
         return {k: round_bf16(v.float()) for k, v in W.items()}
     return {k: v.float() for k, v in W.items()}
 
 
 class _R:
-    """Rounding points of one regime."""
+    """Rounding points of one regime. "int8" is the bf16 regime with the DiT
+    after quantize_dit_ (D/int8_dit.py:71-85): every linear with
+    min(in, out) >= 512 is an Int8DynamicLinear (D/int8_dit.py:34-65)."""
+
+    INT8_MIN_FEATURES = 512
 
     def __init__(self, regime: str):
-        if regime not in ("fp32", "bf16"):
+        if regime not in ("fp32", "bf16", "int8"):
             raise ValueError(regime)
-        self.bf16 = regime == "bf16"
+        self.bf16 = regime in ("bf16", "int8")
+        self.int8 = regime == "int8"
+        self._wq = {}
 
     def r(self, t):
         return round_bf16(t) if self.bf16 else t
 
     def linear(self, x, w, b=None):
         """nn.Linear under autocast: bf16 operands, fp32 accumulate, +bias,
-        one rounding (cuBLAS/hipBLASLt bias epilogue)."""
+        one rounding (cuBLAS/hipBLASLt bias epilogue); in the int8 regime an
+        eligible weight goes through the W8A8 linear instead."""
+        if self.int8 and min(w.shape) >= self.INT8_MIN_FEATURES:
+            return self._int8_linear(x, w, b)
         y = torch.matmul(self.r(x), w.t())
         if b is not None:
             y = y + b
         return self.r(y)
+
+    def _int8_linear(self, x, w, b):
+        """Int8DynamicLinear.forward: per-token bf16 activation quantisation,
+        the weight quantised once in float32, the int32 product (exact in
+        float64: |acc| < 2^53) converted to float32 as acc.float() does, then
+        ((acc * s_x) * s_w) + b rounded to bf16 (oracle/int8_ref.py)."""
+        from .int8_ref import dequant, quantize_act, quantize_weight
+        key = (w.data_ptr(), tuple(w.shape))
+        if key not in self._wq:
+            self._wq[key] = quantize_weight(w)
+        Wq, s_w = self._wq[key]
+        shape = x.shape
+        x2 = self.r(x).reshape(-1, shape[-1])
+        q, s_x = quantize_act(x2)
+        acc = (q.double() @ Wq.double().t()).float()
+        y = dequant(acc, s_x, s_w, b)
+        return y.reshape(*shape[:-1], w.shape[0])
 
 
 # --------------------------------------------------------------------------- #
@@ -393,7 +419,7 @@ def pack_fm_inputs(histories: list[torch.Tensor], patch: int, hidden: int, g_con
 def meanflow_grid(num_steps: int, regime: str = "bf16"):
     """``torch.linspace(0, 1, nfe+1)`` in the solver dtype and the per-step
     (t, dt = t[s+1]-t[s]) pairs (D/batched_fm.py:113-116)."""
-    dt_ = torch.bfloat16 if regime == "bf16" else torch.float32
+    dt_ = torch.bfloat16 if regime in ("bf16", "int8") else torch.float32
     times = torch.linspace(0.0, 1.0, num_steps + 1, dtype=dt_)
     ts = [times[s].float().item() for s in range(num_steps)]
     dts = [(times[s + 1] - times[s]).float().item() for s in range(num_steps)]
@@ -536,11 +562,11 @@ def synthetic_requests(n: int, ctx_lo: int, ctx_hi: int, cfg: DitConfig, seed: i
     rn = np.random.RandomState(seed * 4 + 3)
     lens = [int(x) for x in rl.randint(ctx_lo, ctx_hi + 1, size=n)]
     hist = []
-    R = _R(regime)
+    R = _R("bf16" if regime == "int8" else regime)   # hidden_proj is not a DiT linear
     if llm_width is not None:
         hw = torch.from_numpy(init_param("hidden_proj.weight", (cfg.hidden, llm_width), seed))
         hb = torch.from_numpy(init_param("hidden_proj.bias", (cfg.hidden,), seed))
-        if regime == "bf16":
+        if regime in ("bf16", "int8"):
             hw, hb = round_bf16(hw), round_bf16(hb)
     for L in lens:
         if llm_width is None:

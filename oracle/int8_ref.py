@@ -51,7 +51,7 @@ def int_mm_exact(xq: torch.Tensor, Wq: torch.Tensor) -> torch.Tensor:
 def dequant(acc: torch.Tensor, s_x: torch.Tensor, s_w: torch.Tensor, bias):
     """D/int8_dit.py:60-65: ((acc.f32 * s_x) * s_w) + bias.f32 -> bf16 (as
     float32 values); each product and the sum rounded to float32 separately."""
-    out = acc.float() * s_x[:, None]
+    out = acc.float() * s_x.float()[:, None]
     out = out * s_w[None, :]
     if bias is not None:
         out = out + bias.float()[None, :]
