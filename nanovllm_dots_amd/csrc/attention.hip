@@ -34,6 +34,8 @@
 // tiles that cross a row's visible-key limit are masked. exp2 is the hardware
 // v_exp_f32 (results below 2^-126 flush to zero: such weights are below one
 // f32 ulp of the row's largest weight).
+#include <algorithm>
+
 #include "dfh_device.h"
 #include "dfh_kernels.h"
 
@@ -310,53 +312,79 @@ seq_attention_kernel(const uint16_t* __restrict__ qk, long ldqk, const uint16_t*
 // ---------------------------------------------------------------------------
 // Split-KV decode attention for the cached solve: <= 32 queries per sequence,
 // every query sees all kv_len keys (the active rows' mask row in
-// native/model.py:57-75). A workgroup takes DCH keys of one (sequence, head);
-// each wave 64 of them. Each key is used once, so a wave stages only its own
-// 64-key K and V^T tiles: global->LDS DMA moves whole 128-B lines (8 lines per
-// 1 KB instruction), where direct operand loads would touch 32 lines per
-// instruction and every V^T line eight times. The tiles use the swizzle and
-// the key-row permutation of seq_attention_kernel. The four waves' partial
-// softmax states merge in LDS (over the tiles' space); chunks merge in
-// decode_combine_kernel.
-constexpr int DCH = 256;
-constexpr int PART = 32 * 66;  // per chunk: m[32], l[32], O[32][64]
+// native/model.py:57-75). Group g = (sequence, head) is cut into chunks of
+// chunk_keys consecutive keys, one workgroup each, about one workgroup per CU
+// in all. Wave w of a chunk's workgroup takes the chunk's 64-key tiles
+// w, w + 4, ...: it stages each tile's K rows and V^T columns in its own LDS by
+// global->LDS DMA (whole 128-B lines, the swizzle and key-row permutation of
+// seq_attention_kernel), double-buffered, so the next tile streams in while the
+// wave scores this one with the online softmax of seq_attention_kernel (lazy
+// max refresh). Only the wave reads its tiles: no barrier inside the key loop.
+// The four waves' softmax states merge in LDS. A group of one chunk writes its
+// rows there; otherwise each chunk stores its partial (m in log2 units, l, O
+// of its <= 32 queries) and the last chunk of the group to finish merges the
+// group's partials and writes the rows. The chunks of a group are dealt to
+// workgroups with one value of blockIdx.x % 8, which the 8-XCD partition mode
+// places on one XCD: their partials meet in that XCD's L2. A chunk that finds
+// itself on another XCD (hardware register XCC_ID) publishes with an
+// agent-scope release fence and marks the group's counter, and the merging
+// chunk of a marked group takes an agent-scope acquire fence. The last arriver
+// zeroes the counter for the next launch.
+constexpr int DWV = 4;                // waves per workgroup
+constexpr int PART = 32 * 66;         // per chunk: m[32], l[32], O[32][64]
+constexpr int kDecodeMaxChunks = 64;  // chunks per group (merge weights in LDS)
+constexpr int kWaveTile = 2 * BKV * HD;  // K tile then V^T tile, uint16_t elements
 
 __global__ void __launch_bounds__(256)
 decode_attention_kernel(const uint16_t* __restrict__ qk, long ldqk, const uint16_t* __restrict__ vt,
-                        long ld_vt, const AttnSeq* __restrict__ seqs, int heads, float scale_log2,
-                        float* __restrict__ part, int n_chunks, const float* __restrict__ rope_cos,
+                        long ld_vt, const AttnSeq* __restrict__ seqs, int heads, int n_groups, int n_chunks,
+                        int chunk_keys, float scale_log2, float* __restrict__ part, unsigned* __restrict__ cnt,
+                        uint16_t* __restrict__ out, long ldo, const float* __restrict__ rope_cos,
                         const float* __restrict__ rope_sin) {
-  // per wave: K tile [64 keys][64] then V^T tile [64 d][64 keys], 16 KB; after the
-  // scores and P.V the same space holds the waves' O^T for the merge
-  __shared__ __attribute__((aligned(16))) uint16_t tiles[4 * 2 * BKV * HD];
-  __shared__ float Mw[4][32], Lw[4][32];
-  float (*Ow)[HD][33] = reinterpret_cast<float (*)[HD][33]>(tiles);
-  static_assert(sizeof(float) * 4 * HD * 33 <= sizeof(uint16_t) * 4 * 2 * BKV * HD, "merge space");
-  const AttnSeq sq = seqs[blockIdx.z];
-  const int h = blockIdx.y, chunk = blockIdx.x;
+  // per wave two stages of (K tile [64 keys][64], V^T tile [64 d][64 keys]), 32 KB;
+  // after the key loop the wave's first 8.4 KB hold its O^T for the merge
+  __shared__ __attribute__((aligned(16))) uint16_t tiles[DWV * 2 * kWaveTile];
+  __shared__ float Mw[DWV][32], Lw[DWV][32];
+  __shared__ float Ws[kDecodeMaxChunks][32];
+  __shared__ int s_flag;
+  const int xcd = blockIdx.x % NXCD, j = blockIdx.x / NXCD;
+  const int g = xcd + NXCD * (j / n_chunks), chunk = j % n_chunks;
+  if (g >= n_groups) return;  // uniform: padding of the group count to a multiple of 8
+  const int si = g / heads, h = g % heads;
+  const AttnSeq sq = seqs[si];
   const int kv = sq.kv_len;
-  const int k_chunk = chunk * DCH;
-  if (k_chunk >= kv) return;  // uniform: nothing of this sequence here
+  const int k_lo = chunk * chunk_keys;
+  if (k_lo >= kv) return;  // uniform: nothing of this sequence here (not counted below)
+  const int k_hi = min(k_lo + chunk_keys, kv);
+  const int nc = min((kv + chunk_keys - 1) / chunk_keys, n_chunks);  // chunks of this group
   const int H = heads * HD;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l32 = lane & 31, hi = lane >> 5;
   const int nq = sq.q_end - sq.q_begin;
-  const int key0 = k_chunk + wave * BKV;
-  uint16_t* Kw = tiles + wave * 2 * BKV * HD;
-  uint16_t* Vw = Kw + BKV * HD;
-  // DMA: load j fills tile rows [8j, 8j + 8): lane -> row 8j + lane/8, slot lane%8,
+  const int n_t = (k_hi - k_lo + BKV - 1) / BKV;                 // tiles of the chunk
+  const int nw = n_t > wave ? (n_t - wave + DWV - 1) / DWV : 0;  // this wave's tiles
+  uint16_t* st0 = tiles + wave * 2 * kWaveTile;
+  uint16_t* st1 = st0 + kWaveTile;
+  const uint16_t* kbase = qk + (long)sq.kv_row0 * ldqk + H + h * HD;
+  const uint16_t* vbase = vt + (long)(h * HD) * ld_vt + sq.vt_col0;
+  // DMA of the wave's tile i (keys k_lo + (wave + 4i) * 64 + [0, 64)) into a stage:
+  // load j fills tile rows [8j, 8j + 8): lane -> row 8j + lane/8, slot lane%8,
   // which holds source chunk (lane%8) ^ swz(row). K rows past kv_len repeat the
   // last key (masked below); V^T columns past it are finite (zeroed slack)
+  auto dma = [&](uint16_t* stage, int i) {
+    const int key0 = k_lo + (wave + DWV * i) * BKV;
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const int r = j * 8 + (lane >> 3);
-    const int c = (lane & 7) ^ ((r >> 1) & 7);
-    const int key = min(key0 + r, kv - 1);
-    __builtin_amdgcn_global_load_lds(DFH_GPTR(qk + (long)(sq.kv_row0 + key) * ldqk + H + h * HD + c * 8),
-                                     DFH_LPTR(Kw + j * 8 * HD), 16, 0, 0);
-    __builtin_amdgcn_global_load_lds(DFH_GPTR(vt + (long)(h * HD + r) * ld_vt + sq.vt_col0 + key0 + c * 8),
-                                     DFH_LPTR(Vw + j * 8 * BKV), 16, 0, 0);
-  }
+    for (int jj = 0; jj < 8; ++jj) {
+      const int r = jj * 8 + (lane >> 3);
+      const int c = (lane & 7) ^ ((r >> 1) & 7);
+      const int key = min(key0 + r, kv - 1);
+      __builtin_amdgcn_global_load_lds(DFH_GPTR(kbase + (long)key * ldqk + c * 8),
+                                       DFH_LPTR(stage + jj * 8 * HD), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(DFH_GPTR(vbase + (long)r * ld_vt + key0 + c * 8),
+                                       DFH_LPTR(stage + BKV * HD + jj * 8 * BKV), 16, 0, 0);
+    }
+  };
+  if (nw > 0) dma(st0, 0);
   const int qi = l32 < nq ? l32 : nq - 1;
   bf16x8 qf[4];
   {
@@ -365,161 +393,199 @@ decode_attention_kernel(const uint16_t* __restrict__ qk, long ldqk, const uint16
     for (int kk = 0; kk < 4; ++kk) qf[kk] = *reinterpret_cast<const bf16x8*>(qp + 16 * kk);
   }
   if (rope_cos) rope_q(qf, sq.q_begin + qi, hi, rope_cos, rope_sin);  // uniform
-  wait_vm_lgkm0<0>();  // this wave's tiles are in LDS (only this wave reads them)
   const int krow = key_perm(l32);
-  floatx16 s[2];
-#pragma unroll
-  for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-    for (int v = 0; v < 16; ++v) s[kb][v] = 0.f;
-#pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
-      const bf16x8 kf = *reinterpret_cast<const bf16x8*>(Kw + att_off(kb * 32 + krow, 2 * kk + hi));
-      s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[kk], s[kb], 0, 0, 0);
-    }
-  }
-  // accumulator v of block kb holds key key0 + kb*32 + 16*(v/8) + 8*hi + v%8
-  float mx = -INFINITY;
-#pragma unroll
-  for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-    for (int v = 0; v < 16; ++v) {
-      const int key = key0 + kb * 32 + 16 * (v >> 3) + 8 * hi + (v & 7);
-      const float sv = key < kv ? s[kb][v] * scale_log2 : -INFINITY;
-      s[kb][v] = sv;
-      mx = fmaxf(mx, sv);
-    }
-  mx = fmaxf(mx, swap_halves(mx));
-  const float m_safe = mx == -INFINITY ? 0.f : mx;  // a wave entirely past kv_len
-  float psum = 0.f;
-#pragma unroll
-  for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-    for (int v = 0; v < 16; ++v) {
-      const float p = exp2f(s[kb][v] - m_safe);
-      s[kb][v] = p;
-      psum += p;
-    }
-  psum += swap_halves(psum);
   floatx16 o[2];
 #pragma unroll
   for (int b = 0; b < 2; ++b)
 #pragma unroll
     for (int v = 0; v < 16; ++v) o[b][v] = 0.f;
-  // O^T[d][q] += V^T[d][keys] P^T[keys][q]; k-step (kb, half) = keys kb*32 + 16*half + [0, 16)
+  float m_run = -INFINITY, l_run = 0.f;
+  const float thr = kRescaleLog2 / scale_log2;  // in raw score units
+
+  auto compute = [&](const uint16_t* Ks, const uint16_t* Vs, int k0) {
+    floatx16 s[2];
 #pragma unroll
-  for (int kb = 0; kb < 2; ++kb)
+    for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
-    for (int half = 0; half < 2; ++half) {
-      floatx8 pv;
+      for (int v = 0; v < 16; ++v) s[kb][v] = 0.f;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) pv[j] = s[kb][8 * half + j];
-      const bf16x8 pf = __builtin_convertvector(pv, bf16x8);
-#pragma unroll
-      for (int db = 0; db < 2; ++db) {
-        const bf16x8 vf = *reinterpret_cast<const bf16x8*>(Vw + att_off(db * 32 + l32, 4 * kb + 2 * half + hi));
-        o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf, o[db], 0, 0, 0);
+      for (int kk = 0; kk < 4; ++kk) {
+        const bf16x8 kf = *reinterpret_cast<const bf16x8*>(Ks + att_off(kb * 32 + krow, 2 * kk + hi));
+        s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[kk], s[kb], 0, 0, 0);
       }
     }
-  __syncthreads();  // every wave is done with its tiles: their space becomes Ow
-  // O^T[d][q] in lanes: q = l32, d = db*32 + 8*(v/4) + 4*hi + v%4
+    // accumulator v of block kb holds key k0 + kb*32 + 16*(v/8) + 8*hi + v%8
+    if (k0 + BKV > kv) {  // wave-uniform: the sequence's last tile
+      const int rel = kv - k0 - 8 * hi;
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int v = 0; v < 16; ++v)
+          if (kb * 32 + 16 * (v >> 3) + (v & 7) >= rel) s[kb][v] = -INFINITY;
+    }
+    float mx = fmaxf(s[0][0], s[0][1]);
+#pragma unroll
+    for (int v = 2; v < 16; ++v) mx = fmaxf(mx, s[0][v]);
+#pragma unroll
+    for (int v = 0; v < 16; ++v) mx = fmaxf(mx, s[1][v]);
+    mx = fmaxf(mx, swap_halves(mx));  // finite: every tile holds a key below kv_len
+    if (__any(mx > m_run + thr)) {
+      const float m_new = fmaxf(m_run, mx);
+      const float alpha = __builtin_amdgcn_exp2f((m_run - m_new) * scale_log2);
+      m_run = m_new;
+      l_run *= alpha;
+#pragma unroll
+      for (int b = 0; b < 2; ++b)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) o[b][v] *= alpha;
+    }
+    const float mb = m_run * scale_log2;
+    float psum = 0.f;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kb][v], scale_log2, -mb));
+        s[kb][v] = p;
+        psum += p;
+      }
+    l_run += psum;
+    // O^T[d][q] += V^T[d][keys] P^T[keys][q]; k-step (kb, half) = keys kb*32 + 16*half + [0, 16)
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+        floatx8 pv;
+#pragma unroll
+        for (int jv = 0; jv < 8; ++jv) pv[jv] = s[kb][8 * half + jv];
+        const bf16x8 pf = __builtin_convertvector(pv, bf16x8);
+#pragma unroll
+        for (int db = 0; db < 2; ++db) {
+          const bf16x8 vf =
+              *reinterpret_cast<const bf16x8*>(Vs + att_off(db * 32 + l32, 4 * kb + 2 * half + hi));
+          o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf, o[db], 0, 0, 0);
+        }
+      }
+  };
+
+  // Tile i sits in stage i % 2. At the top of step i the wave waits for tile i
+  // (its only outstanding DMA) and for its LDS reads of tile i - 1, then starts
+  // tile i + 1 into the stage tile i - 1 used.
+  for (int i = 0; i < nw; i += 2) {
+    wait_vm_lgkm0<0>();
+    if (i + 1 < nw) dma(st1, i + 1);
+    compute(st0, st0 + BKV * HD, k_lo + (wave + DWV * i) * BKV);
+    if (i + 1 >= nw) break;
+    wait_vm_lgkm0<0>();
+    if (i + 2 < nw) dma(st0, i + 2);
+    compute(st1, st1 + BKV * HD, k_lo + (wave + DWV * (i + 1)) * BKV);
+  }
+  wait_vm_lgkm0<0>();  // (a wave without tiles) nothing outstanding into its stages
+  // O^T[d][q] in lanes: q = l32, d = db*32 + 8*(v/4) + 4*hi + v%4; the wave's own stage space
+  float (*Ow)[33] = reinterpret_cast<float (*)[33]>(st0);
+  static_assert(sizeof(float) * HD * 33 <= sizeof(uint16_t) * 2 * kWaveTile, "merge space");
 #pragma unroll
   for (int db = 0; db < 2; ++db)
 #pragma unroll
-    for (int v = 0; v < 16; ++v) Ow[wave][db * 32 + 8 * (v >> 2) + 4 * hi + (v & 3)][l32] = o[db][v];
+    for (int v = 0; v < 16; ++v) Ow[db * 32 + 8 * (v >> 2) + 4 * hi + (v & 3)][l32] = o[db][v];
+  const float l_tot = l_run + swap_halves(l_run);
   if (hi == 0) {
-    Mw[wave][l32] = mx;
-    Lw[wave][l32] = psum;
+    Mw[wave][l32] = nw > 0 ? m_run * scale_log2 : -INFINITY;
+    Lw[wave][l32] = l_tot;
   }
   __syncthreads();
-  float* pp = part + ((long)(blockIdx.z * heads + h) * n_chunks + chunk) * PART;
-  if (tid < 32) {
-    float M = -INFINITY;
+  auto ow = [&](int w) { return reinterpret_cast<const float (*)[33]>(tiles + w * 2 * kWaveTile); };
+  // merge of the four waves for query q: max M, weight of wave w = exp2(m_w - M)
+  auto wave_merge = [&](int q, float& M, float (&wt)[DWV]) {
+    M = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < 4; ++w) M = fmaxf(M, Mw[w][tid]);
-    float L = 0.f;
+    for (int w = 0; w < DWV; ++w) M = fmaxf(M, Mw[w][q]);
 #pragma unroll
-    for (int w = 0; w < 4; ++w)
-      if (Mw[w][tid] != -INFINITY) L += Lw[w][tid] * exp2f(Mw[w][tid] - M);
-    pp[tid] = M;
-    pp[32 + tid] = L;
-  }
-  for (int e = tid; e < 32 * HD; e += 256) {
-    const int q = e / HD, d = e % HD;
-    float M = -INFINITY;
+    for (int w = 0; w < DWV; ++w) wt[w] = Mw[w][q] != -INFINITY ? __builtin_amdgcn_exp2f(Mw[w][q] - M) : 0.f;
+  };
+  if (nc == 1) {  // the group's only chunk: normalised rows straight out
+    for (int e = tid; e < nq * (HD / 2); e += 256) {
+      const int q = e / (HD / 2), d = 2 * (e % (HD / 2));
+      float M, wt[DWV];
+      wave_merge(q, M, wt);
+      float L = 0.f, o0 = 0.f, o1 = 0.f;
 #pragma unroll
-    for (int w = 0; w < 4; ++w) M = fmaxf(M, Mw[w][q]);
-    float O = 0.f;
-#pragma unroll
-    for (int w = 0; w < 4; ++w)
-      if (Mw[w][q] != -INFINITY) O += Ow[w][d][q] * exp2f(Mw[w][q] - M);
-    pp[64 + q * HD + d] = O;
-  }
-}
-
-// Merge of the chunk partials: one workgroup per (sequence, head, group of
-// DQG queries). Per block of up to DCB chunks, the chunk weights
-// exp2(m_c - M) / L of the group's queries go to LDS; then every thread adds
-// two output columns of one query over the block's chunks with independent
-// loads (64 threads per query read its 256-B O rows coalesced).
-constexpr int DQG = 8;    // queries per combine workgroup
-constexpr int DCB = 256;  // chunks per LDS block of weights
-
-__global__ void __launch_bounds__(256)
-decode_combine_kernel(const float* __restrict__ part, const AttnSeq* __restrict__ seqs, int heads,
-                      int n_chunks, uint16_t* __restrict__ out, long ldo) {
-  __shared__ float Ws[DQG][DCB];
-  __shared__ float Mq[DQG], Lq[DQG];
-  const AttnSeq sq = seqs[blockIdx.y];
-  const int h = blockIdx.x, qg = blockIdx.z * DQG;
-  const int nq = sq.q_end - sq.q_begin;
-  if (qg >= nq) return;  // uniform
-  const int R = min(DQG, nq - qg);
-  const int nc = min((sq.kv_len + DCH - 1) / DCH, n_chunks);
-  const float* pp = part + (long)(blockIdx.y * heads + h) * n_chunks * PART;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  // row max and sum of each query over all chunks: wave w takes queries w and w + 4
-  for (int r = wave; r < R; r += 4) {
-    const int q = qg + r;
-    float M = -INFINITY;
-    for (int c = lane; c < nc; c += 64) M = fmaxf(M, pp[(long)c * PART + q]);
-    M = wave_max(M);
-    float L = 0.f;
-    if (M != -INFINITY)
-      for (int c = lane; c < nc; c += 64) {
-        const float mc = pp[(long)c * PART + q];
-        if (mc != -INFINITY) L += pp[(long)c * PART + 32 + q] * exp2f(mc - M);
+      for (int w = 0; w < DWV; ++w) {
+        L += Lw[w][q] * wt[w];
+        o0 += ow(w)[d][q] * wt[w];
+        o1 += ow(w)[d + 1][q] * wt[w];
       }
-    L = wave_sum(L);
-    if (lane == 0) { Mq[r] = M; Lq[r] = L; }
+      const float inv = 1.0f / L;
+      *reinterpret_cast<uint32_t*>(out + (long)(sq.out_row0 + sq.q_begin + q) * ldo + h * HD + d) =
+          pack2(o0 * inv, o1 * inv);
+    }
+    return;
+  }
+  float* pg = part + (long)g * n_chunks * PART;  // the group's partials
+  {
+    float* pp = pg + (long)chunk * PART;
+    if (tid < nq) {
+      float M, wt[DWV];
+      wave_merge(tid, M, wt);
+      float L = 0.f;
+#pragma unroll
+      for (int w = 0; w < DWV; ++w) L += Lw[w][tid] * wt[w];
+      pp[tid] = M;
+      pp[32 + tid] = L;
+    }
+    for (int e = tid; e < nq * HD; e += 256) {
+      const int q = e / HD, d = e % HD;
+      float M, wt[DWV];
+      wave_merge(q, M, wt);
+      float O = 0.f;
+#pragma unroll
+      for (int w = 0; w < DWV; ++w) O += ow(w)[d][q] * wt[w];
+      pp[64 + q * HD + d] = O;
+    }
+  }
+  const bool on_xcd = __builtin_amdgcn_s_getreg((3 << 11) | 20) == xcd;  // hwreg(XCC_ID, 0, 4); uniform
+  if (!on_xcd) __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's partial stores are in L2
+  __syncthreads();                                   // ... and every wave's
+  if (tid == 0) {
+    const unsigned add = on_xcd ? 1u : 0x10001u;
+    const unsigned now = __hip_atomic_fetch_add(cnt + g, add, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + add;
+    s_flag = (now & 0xffffu) != (unsigned)nc ? 0 : (now >> 16) ? 2 : 1;
   }
   __syncthreads();
-  const int r = tid >> 5, d = (tid & 31) * 2;  // this thread's query and two output columns
-  float o0 = 0.f, o1 = 0.f;
-  for (int c0 = 0; c0 < nc; c0 += DCB) {
-    const int cn = min(DCB, nc - c0);
-    for (int idx = tid; idx < R * cn; idx += 256) {
-      const int rr = idx / cn, cc = idx % cn;
-      const float mc = pp[(long)(c0 + cc) * PART + qg + rr];
-      const float M = Mq[rr], L = Lq[rr];
-      Ws[rr][cc] = (L > 0.f && mc != -INFINITY) ? exp2f(mc - M) / L : 0.f;
+  if (!s_flag) return;  // uniform
+  if (s_flag == 2) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  asm volatile("" ::: "memory");
+  if (tid == 0) cnt[g] = 0u;  // ready for the next launch
+  // Last chunk in: per query the chunk weights exp2(m_c - M) / L go to LDS, then
+  // every thread adds two output columns of one query over the chunks in chunk order.
+  if (tid < nq) {
+    float M = -INFINITY;
+    for (int c = 0; c < nc; ++c) M = fmaxf(M, pg[(long)c * PART + tid]);
+    float L = 0.f;
+    for (int c = 0; c < nc; ++c) {
+      const float mc = pg[(long)c * PART + tid];
+      if (mc != -INFINITY) L += pg[(long)c * PART + 32 + tid] * __builtin_amdgcn_exp2f(mc - M);
     }
-    __syncthreads();
-    if (r < R) {
-      const float* po = pp + (long)c0 * PART + 64 + (qg + r) * HD + d;
-#pragma unroll 8
-      for (int cc = 0; cc < cn; ++cc) {
-        const float w = Ws[r][cc];
-        const float2 x = *reinterpret_cast<const float2*>(po + (long)cc * PART);
-        o0 += w != 0.f ? w * x.x : 0.f;
-        o1 += w != 0.f ? w * x.y : 0.f;
-      }
+    const float inv = 1.0f / L;
+    for (int c = 0; c < nc; ++c) {
+      const float mc = pg[(long)c * PART + tid];
+      Ws[c][tid] = mc != -INFINITY ? __builtin_amdgcn_exp2f(mc - M) * inv : 0.f;
     }
-    __syncthreads();
   }
-  if (r < R)
-    *reinterpret_cast<uint32_t*>(out + (long)(sq.out_row0 + sq.q_begin + qg + r) * ldo + h * HD + d) =
-        pack2(o0, o1);
+  __syncthreads();
+  for (int e = tid; e < nq * (HD / 2); e += 256) {
+    const int q = e / (HD / 2), d = 2 * (e % (HD / 2));
+    const float* po = pg + 64 + q * HD + d;
+    float o0 = 0.f, o1 = 0.f;
+    for (int c = 0; c < nc; ++c) {
+      const float w = Ws[c][q];
+      const float2 x = *reinterpret_cast<const float2*>(po + (long)c * PART);
+      o0 += w * x.x;
+      o1 += w * x.y;
+    }
+    *reinterpret_cast<uint32_t*>(out + (long)(sq.out_row0 + sq.q_begin + q) * ldo + h * HD + d) = pack2(o0, o1);
+  }
 }
 
 }  // namespace
@@ -544,17 +610,30 @@ hipError_t seq_attention(const uint16_t* qk, long ldqk, const uint16_t* vt, long
 
 hipError_t decode_attention(const uint16_t* qk, long ldqk, const uint16_t* vt, long ld_vt, uint16_t* out,
                             long ldo, const AttnSeq* seqs, int n_seq, int heads, int max_kv,
-                            float* part, const float* rope_cos, const float* rope_sin, hipStream_t s) {
+                            float* part, unsigned* counters, const float* rope_cos, const float* rope_sin,
+                            hipStream_t s) {
   if (n_seq <= 0 || max_kv <= 0) return hipSuccess;
   const float scale_log2 = 0.125f * 1.4426950408889634f;
-  const int n_chunks = (max_kv + DCH - 1) / DCH;
-  dfh_launch(decode_attention_kernel, dim3(n_chunks, heads, n_seq), dim3(256), 0, s, qk, ldqk, vt, ld_vt,
-             seqs, heads, scale_log2, part, n_chunks, rope_cos, rope_sin);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(decode_combine_kernel, dim3(heads, n_seq, 32 / DQG), dim3(256), 0, s, part, seqs, heads,
-                     n_chunks, out, ldo);
+  const DecodeSplit sp = decode_split(n_seq, heads, max_kv);
+  const long groups8 = ((long)n_seq * heads + NXCD - 1) / NXCD * NXCD;
+  if (groups8 * sp.n_chunks > 0x7fffffffL) return hipErrorInvalidValue;
+  dfh_launch(decode_attention_kernel, dim3((unsigned)(groups8 * sp.n_chunks)), dim3(256), 0, s, qk, ldqk, vt,
+             ld_vt, seqs, heads, n_seq * heads, sp.n_chunks, sp.chunk_keys, scale_log2, part, counters, out, ldo,
+             rope_cos, rope_sin);
   return hipGetLastError();
+}
+
+DecodeSplit decode_split(int n_seq, int heads, int max_kv) {
+  // about one workgroup per CU (each holds 128 KB of LDS), chunks of whole
+  // 256-key rounds (one 64-key tile per wave)
+  const long groups = (long)n_seq * heads;
+  int want = (int)(cu_count() / (groups > 0 ? groups : 1));
+  const int rounds = (max_kv + DWV * BKV - 1) / (DWV * BKV);
+  want = std::max(1, std::min(std::min(want, rounds), kDecodeMaxChunks));
+  DecodeSplit sp;
+  sp.chunk_keys = (rounds + want - 1) / want * (DWV * BKV);
+  sp.n_chunks = (max_kv + sp.chunk_keys - 1) / sp.chunk_keys;
+  return sp;
 }
 
 }  // namespace dfh

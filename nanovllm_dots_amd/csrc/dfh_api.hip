@@ -360,6 +360,7 @@ struct Pass {
   int n_seq = 0, max_q = 0, max_kv = 0;
   bool decode = false;         // split-KV decode attention (<= 32 queries / sequence)
   float* part = nullptr;       // decode partials
+  unsigned* part_cnt = nullptr;  // decode merge counters (zero between launches)
   bool kv_only_last = false;   // prefix pass: the last block only has to leave its K/V
   // input_layer rows computed before the pass (solve: the history rows once per
   // solve, the latent rows per step): block 0 reads them and writes h->x
@@ -470,7 +471,7 @@ int run_blocks(DfhHandle* h, const Pass& p, hipStream_t s) {
     prof_arm(h, PC_ATTN);
     if (p.decode)
       DFH_CHECK(decode_attention(p.qk[l], p.ldqk, p.vt[l], p.ld_vt, P<uint16_t>(h->attn), H, p.seqs, p.n_seq,
-                                 c.heads, p.max_kv, p.part, aq_cos, aq_sin, s));
+                                 c.heads, p.max_kv, p.part, p.part_cnt, aq_cos, aq_sin, s));
     else
       DFH_CHECK(seq_attention(p.qk[l], p.ldqk, p.vt[l], p.ld_vt, P<uint16_t>(h->attn), H, c.heads, h->attq.p,
                               (long)p.n_seq * ((p.max_q + 127) / 128), aq_cos, aq_sin, s));
@@ -1110,10 +1111,11 @@ int dfh_gemm_w8a8_ws(const void* xq, long ldx, const void* wq, long ldw, void* o
 // at timestep k, followed by scratch slots for the step's active rows.
 struct DfhKVCache {
   DfhHandle* h = nullptr;
-  int n = 0, S = 0, cap = 0;
+  int n = 0, S = 0, cap = 0;  // cap: region stride (the capacity rounded up to 64 keys)
+  int capacity = 0;           // rows a stream may hold, prefix + active block
   long rows_total = 0, ld_vt = 0;
   std::vector<DevBuf> qk, vt;
-  DevBuf lens, counts, offs, seqs, c_rows, row_req, row_pos, vt_col, patch_rows, lh_rows, part, z;
+  DevBuf lens, counts, offs, seqs, c_rows, row_req, row_pos, vt_col, patch_rows, lh_rows, part, part_cnt, z;
   long table_rows = 0;
   std::vector<int> lens_host;
   int* pinned = nullptr;  // 2n+1 ints staged for uploads
@@ -1216,6 +1218,7 @@ int cache_solve(DfhKVCache* c, const uint16_t* last_hidden, const int* lh_src_ro
     p.max_kv = max_len + R;
     p.decode = true;
     p.part = P<float>(c->part);
+    p.part_cnt = P<unsigned>(c->part_cnt);
     if (run_blocks(h, p, s)) return 1;
     const uint16_t* mf = P<uint16_t>(h->mod) + (long)cf.n_blocks * 6 * H;
     prof_arm(h, PC_LN);
@@ -1240,6 +1243,10 @@ int cache_alloc(DfhHandle* h, int n, int cap, int S, DfhKVCache** out) {
   auto bail = [&](hipError_t e) {
     for (auto& b : c->qk) if (b.p) (void)hipFree(b.p);
     for (auto& b : c->vt) if (b.p) (void)hipFree(b.p);
+    DevBuf* bufs[] = {&c->lens, &c->counts, &c->offs, &c->seqs, &c->patch_rows, &c->lh_rows, &c->part,
+                      &c->part_cnt, &c->z};
+    for (DevBuf* b : bufs) if (b->p) (void)hipFree(b->p);
+    if (c->pinned) (void)hipHostFree(c->pinned);
     delete c;
     return fail("kv cache allocation: %s", hipGetErrorString(e));
   };
@@ -1258,6 +1265,8 @@ int cache_alloc(DfhHandle* h, int n, int cap, int S, DfhKVCache** out) {
   if (e == hipSuccess) e = dev_alloc(c->patch_rows, (size_t)n * cf.patch * 4);
   if (e == hipSuccess) e = dev_alloc(c->lh_rows, (size_t)n * 4);
   if (e == hipSuccess) e = dev_alloc(c->part, (size_t)n * cf.heads * n_chunks * 32 * 66 * 4);
+  if (e == hipSuccess) e = dev_alloc(c->part_cnt, (size_t)n * cf.heads * 4);
+  if (e == hipSuccess) e = hipMemset(c->part_cnt.p, 0, (size_t)n * cf.heads * 4);
   if (e == hipSuccess) e = dev_alloc(c->z, (size_t)n * cf.patch * cf.latent_dim * 2);
   if (e == hipSuccess) e = hipHostMalloc(reinterpret_cast<void**>(&c->pinned), (2 * n + 2) * sizeof(int));
   if (e != hipSuccess) return bail(e);
@@ -1281,10 +1290,13 @@ int dfh_kvcache_create(DfhHandle* h, int n_streams, int capacity, int num_steps,
   if (h->cfg.patch + 1 > 32)
     return fail("dfh_kvcache_create: latent patch %d too large (1 + patch active rows must be <= 32)",
                 h->cfg.patch);
-  const int cap = (capacity + 7) & ~7;  // region starts stay 16-byte aligned in V^T
+  // region starts at multiples of 64 keys: a 64-key V^T row segment is one 128-B line
+  const int cap = (capacity + 63) & ~63;
   if ((long)num_steps * n_streams * cap * 2 * h->cfg.hidden >= (1L << 31))
     return fail("dfh_kvcache_create: cache too large for 32-bit offsets");
-  return cache_alloc(h, n_streams, cap, num_steps, out);
+  if (cache_alloc(h, n_streams, cap, num_steps, out)) return 1;
+  (*out)->capacity = capacity;
+  return 0;
 }
 
 int dfh_kvcache_destroy(DfhKVCache* c) {
@@ -1293,7 +1305,7 @@ int dfh_kvcache_destroy(DfhKVCache* c) {
   for (auto& b : c->qk) if (b.p) (void)hipFree(b.p);
   for (auto& b : c->vt) if (b.p) (void)hipFree(b.p);
   DevBuf* bufs[] = {&c->lens, &c->counts, &c->offs, &c->seqs, &c->c_rows, &c->row_req, &c->row_pos,
-                    &c->vt_col, &c->patch_rows, &c->lh_rows, &c->part, &c->z};
+                    &c->vt_col, &c->patch_rows, &c->lh_rows, &c->part, &c->part_cnt, &c->z};
   for (DevBuf* b : bufs) if (b->p) (void)hipFree(b->p);
   if (c->pinned) (void)hipHostFree(c->pinned);
   delete c;
@@ -1321,9 +1333,9 @@ int dfh_kvcache_extend(DfhKVCache* c, const void* rows, int m_max, const int* co
   int Mtot = 0, max_count = 0;
   for (int i = 0; i < c->n; ++i) {
     if (counts[i] < 0 || counts[i] > m_max) return fail("dfh_kvcache_extend: counts[%d]=%d", i, counts[i]);
-    if (c->lens_host[i] + counts[i] + R > c->cap)
+    if (c->lens_host[i] + counts[i] + R > c->capacity)
       return fail("dfh_kvcache_extend: stream %d would hold %d rows (+%d active) > capacity %d", i,
-                  c->lens_host[i] + counts[i], R, c->cap);
+                  c->lens_host[i] + counts[i], R, c->capacity);
     Mtot += counts[i];
     max_count = counts[i] > max_count ? counts[i] : max_count;
   }
@@ -1351,7 +1363,7 @@ int dfh_kvcache_solve(DfhKVCache* c, const void* last_hidden, const void* g_cond
   const int R = 1 + c->h->cfg.patch;
   int max_len = 0;
   for (int i = 0; i < c->n; ++i) {
-    if (c->lens_host[i] + R > c->cap) return fail("dfh_kvcache_solve: stream %d prefix too long", i);
+    if (c->lens_host[i] + R > c->capacity) return fail("dfh_kvcache_solve: stream %d prefix too long", i);
     max_len = c->lens_host[i] > max_len ? c->lens_host[i] : max_len;
   }
   TimeVals tv{}, dtv{};

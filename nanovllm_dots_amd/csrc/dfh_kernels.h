@@ -130,12 +130,23 @@ hipError_t seq_attention(const uint16_t* qk, long ldqk, const uint16_t* vt, long
                          const float* rope_sin, hipStream_t s);
 
 // Split-KV decode attention: every query of a sequence sees all kv_len keys
-// (q_begin..q_end are at most 32 queries). Keys are read straight from HBM in
-// chunks of kv_chunk keys per workgroup; partials go to `part` and are merged.
-// part holds n_seq * heads * ceil(max_kv / kv_chunk) * 32 * 66 floats.
+// (q_begin..q_end are at most 32 queries). Each (sequence, head) is cut into
+// decode_split(...).n_chunks chunks of keys read straight from HBM, one
+// workgroup each; the last chunk of a (sequence, head) to finish merges the
+// chunk partials in `part` and writes the rows. part holds
+// n_seq * heads * n_chunks * 32 * 66 floats (n_chunks <= ceil(max_kv / 256));
+// counters holds n_seq * heads zeroed words and is left zeroed by every launch.
+struct DecodeSplit {
+  int n_chunks = 1, chunk_keys = 256;
+};
+DecodeSplit decode_split(int n_seq, int heads, int max_kv);
 hipError_t decode_attention(const uint16_t* qk, long ldqk, const uint16_t* vt, long ld_vt, uint16_t* out,
                             long ldo, const AttnSeq* seqs, int n_seq, int heads, int max_kv,
-                            float* part, const float* rope_cos, const float* rope_sin, hipStream_t s);
+                            float* part, unsigned* counters, const float* rope_cos, const float* rope_sin,
+                            hipStream_t s);
+
+// compute units of the current device (queried once)
+int cu_count();
 
 // Paged attention of appended tokens over a paged (or contiguous) KV cache
 // (flash_attn_varlen_func / flash_attn_with_kvcache semantics, bottom-right

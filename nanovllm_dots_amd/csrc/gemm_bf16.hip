@@ -997,6 +997,11 @@ gemm_mfma_kernel(GemmArgs a) {
   auto part_off = [&](int i, int k, int q) {
     return (((((long)wave * C::RN + i) * C::RM + k) * 4 + q) * 64 + lane) * 4;
   };
+  // a lane's accumulators belong to one output row; rows at or past M are
+  // neither stored nor summed (the epilogue drops them)
+  int pm0, pn0;
+  tile_mn(tile_p, pm0, pn0);
+  auto row_ok = [&](int k) { return pm0 + wm * C::WTM + k * 32 + l32 < M; };
   {
     float* wp = a.ws + kSplitCounters + (long)(xcd * per_xcd + piece) * (BM * BN);
 #pragma unroll
@@ -1008,7 +1013,8 @@ gemm_mfma_kernel(GemmArgs a) {
           // copy the elements out first: a bit_cast of a vector-element expression reads element 0
           const E e0 = acc[i][k][4 * q], e1 = acc[i][k][4 * q + 1], e2 = acc[i][k][4 * q + 2],
                   e3 = acc[i][k][4 * q + 3];
-          *reinterpret_cast<float4*>(wp + part_off(i, k, q)) =
+          if (row_ok(k))
+            *reinterpret_cast<float4*>(wp + part_off(i, k, q)) =
               make_float4(__builtin_bit_cast(float, e0), __builtin_bit_cast(float, e1),
                           __builtin_bit_cast(float, e2), __builtin_bit_cast(float, e3));
         }
@@ -1043,9 +1049,10 @@ gemm_mfma_kernel(GemmArgs a) {
   const float* wbase = a.ws + kSplitCounters + (long)(xcd * per_xcd + tt * split) * (BM * BN);
   auto load_block = [&](int kc, int i, int k, E (&x)[16]) {
     const float* wp = wbase + (long)kc * (BM * BN);
+    const bool ok = row_ok(k);
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      const float4 v = *reinterpret_cast<const float4*>(wp + part_off(i, k, q));
+      const float4 v = ok ? *reinterpret_cast<const float4*>(wp + part_off(i, k, q)) : make_float4(0.f, 0.f, 0.f, 0.f);
       x[4 * q] = __builtin_bit_cast(E, v.x);
       x[4 * q + 1] = __builtin_bit_cast(E, v.y);
       x[4 * q + 2] = __builtin_bit_cast(E, v.z);
@@ -1136,12 +1143,19 @@ using T6 = Cfg<256, 128, 64, 3, 2, 2>;  // 4 waves, 3 stages, 144 KB
 using T7 = Cfg<128, 128, 32, 4, 2, 2>;  // 4 waves, 4 stages of BK 32, 64 KB: two per CU
 using T8 = Cfg<256, 256, 64, 2, 2, 4, 1>;  // T0 with the DMA of a step issued by one half
 using T9 = Cfg<256, 256, 32, 5, 2, 2, 2>;  // 4 waves, 128x128 per wave (AGPRs), DMA spread over the MFMAs, 160 KB
-constexpr int kNumTiles = 10;
-const int kTileBM[kNumTiles] = {T0::BM, T1::BM, T2::BM, T3::BM, T4::BM, T5::BM, T6::BM, T7::BM, T8::BM, T9::BM};
-const int kTileBN[kNumTiles] = {T0::BN, T1::BN, T2::BN, T3::BN, T4::BN, T5::BN, T6::BN, T7::BN, T8::BN, T9::BN};
-const int kTileBK[kNumTiles] = {T0::BK, T1::BK, T2::BK, T3::BK, T4::BK, T5::BK, T6::BK, T7::BK, T8::BK, T9::BK};
-const int kTileWTN[kNumTiles] = {T0::WTN, T1::WTN, T2::WTN, T3::WTN, T4::WTN, T5::WTN, T6::WTN, T7::WTN,
-                                 T8::WTN, T9::WTN};
+// at most 128 rows (a decode-sized batch): one row block, narrow column blocks
+// and K pieces spread the weights over the whole chip; two workgroups per CU
+using T10 = Cfg<128, 32, 64, 4, 4, 1>;  // 4 waves, 32x32 per wave, 80 KB
+using T11 = Cfg<128, 64, 64, 3, 4, 1>;  // 4 waves, 32x64 per wave (RoPE pairs of the QKV epilogue), 72 KB
+constexpr int kNumTiles = 12;
+const int kTileBM[kNumTiles] = {T0::BM, T1::BM, T2::BM, T3::BM, T4::BM,  T5::BM,
+                                T6::BM, T7::BM, T8::BM, T9::BM, T10::BM, T11::BM};
+const int kTileBN[kNumTiles] = {T0::BN, T1::BN, T2::BN, T3::BN, T4::BN,  T5::BN,
+                                T6::BN, T7::BN, T8::BN, T9::BN, T10::BN, T11::BN};
+const int kTileBK[kNumTiles] = {T0::BK, T1::BK, T2::BK, T3::BK, T4::BK,  T5::BK,
+                                T6::BK, T7::BK, T8::BK, T9::BK, T10::BK, T11::BK};
+const int kTileWTN[kNumTiles] = {T0::WTN, T1::WTN, T2::WTN, T3::WTN, T4::WTN,  T5::WTN,
+                                 T6::WTN, T7::WTN, T8::WTN, T9::WTN, T10::WTN, T11::WTN};
 
 template <class Op, int EPI>
 hipError_t dispatch_tiles(const GemmArgs& a, hipStream_t s, int tile) {
@@ -1156,12 +1170,15 @@ hipError_t dispatch_tiles(const GemmArgs& a, hipStream_t s, int tile) {
     case 7: return launch<T7, Op, EPI>(a, s);
     case 8: return launch<T8, Op, EPI>(a, s);
     case 9: return launch<T9, Op, EPI>(a, s);
+    case 10: return launch<T10, Op, EPI>(a, s);
+    case 11: return launch<T11, Op, EPI>(a, s);
     default: return hipErrorInvalidValue;
   }
 }
 
 int pick_tile(const GemmArgs& a) {
   const long cus = num_cus();
+  if (a.M <= 128 && a.N % 32 == 0 && a.K % 64 == 0) return 10;
   const long t0 = (long)((a.M + 255) / 256) * (a.N / 256);
   if (a.N % 256 == 0 && a.K % 64 == 0 && t0 >= 2 * cus) return 8;
   if (a.N % 128 == 0 && a.K % 64 == 0 && (long)((a.M + 127) / 128) * (a.N / 128) >= cus) return 2;
@@ -1170,12 +1187,14 @@ int pick_tile(const GemmArgs& a) {
 
 }  // namespace
 
+int cu_count() { return num_cus(); }
+
 hipError_t gemm_bf16(const GemmArgs& a, int epi, hipStream_t s, int tile) {
   if (a.K <= 0 || a.N <= 0 || a.M < 0 || a.K % 32 != 0) return hipErrorInvalidValue;
   if (a.M == 0) return hipSuccess;  // a.M is the host upper bound of rows
   if (tile < 0) tile = pick_tile(a);
   if (tile < 0 || tile >= kNumTiles) return hipErrorInvalidValue;
-  if (epi == EPI_QKV && kTileWTN[tile] < 64) tile = 2;  // RoPE pairs need a 64-column wave tile
+  if (epi == EPI_QKV && kTileWTN[tile] < 64) tile = a.M <= 128 ? 11 : 2;  // RoPE pairs need a 64-column wave tile
   if (a.N % kTileBN[tile] != 0 || a.K % kTileBK[tile] != 0) return hipErrorInvalidValue;
   if (epi == EPI_QKV && (a.hidden % kTileBN[tile] != 0 || a.head_dim != 64)) return hipErrorInvalidValue;
   // element offsets are 32-bit
@@ -1204,7 +1223,7 @@ hipError_t gemm_i8(const GemmArgs& a_bytes, int epi, hipStream_t s, int tile) {
   a.ldb = a_bytes.ldb / 2;
   if (tile < 0) tile = pick_tile(a);
   if (tile < 0 || tile >= kNumTiles) return hipErrorInvalidValue;
-  if (epi == EPI_DQ_QKV && kTileWTN[tile] < 64) tile = 2;  // RoPE pairs need a 64-column wave tile
+  if (epi == EPI_DQ_QKV && kTileWTN[tile] < 64) tile = a.M <= 128 ? 11 : 2;  // RoPE pairs need a 64-column wave tile
   if (a.N % kTileBN[tile] != 0 || a.K % kTileBK[tile] != 0) return hipErrorInvalidValue;
   if (epi == EPI_DQ_QKV && (a.hidden % kTileBN[tile] != 0 || a.head_dim != 64)) return hipErrorInvalidValue;
   if (is_dq(epi) && (!a.sx || !a.sw)) return hipErrorInvalidValue;

@@ -139,3 +139,27 @@ def test_ksplit_matches_whole_tiles(path):
         outs.append(out)
     head.set_ksplit(True)
     _check(outs[1], outs[0], CFG.latent_dim, f"ksplit-vs-whole {path}")
+
+
+def test_decode_chunks_ragged_streams_and_repeated_solves():
+    """Streams whose prefixes span one to 13 key chunks in one launch (a stream
+    of one chunk writes its rows directly, the others merge their chunk
+    partials in the last chunk to finish), a group count (3 streams x 4 heads)
+    that is not a multiple of 8, and solves repeated on the same cache: the
+    merge counters return to zero and the chunk-order merge repeats bit for bit."""
+    from nanovllm_dots_amd import HipFMCache
+    head, Wb = _head(CFG, 3)
+    rs = np.random.RandomState(21)
+    hist = [R.round_bf16(torch.from_numpy((0.5 * rs.standard_normal((n, CFG.hidden))).astype(np.float32)))
+            for n in (41, 1500, 3101)]
+    noise = R.round_bf16(torch.from_numpy(rs.standard_normal((3, CFG.patch, CFG.latent_dim)).astype(np.float32)))
+    ref = R.meanflow_solve_varlen(Wb, CFG, hist, None, noise, 4, "bf16")
+    cache = HipFMCache(head, 3, 3136, 4)
+    prefix = [h[:-1] for h in hist]
+    cache.extend(_pad(prefix, CFG.hidden).cuda(), [p.shape[0] for p in prefix])
+    lh = torch.stack([h[-1] for h in hist]).cuda()
+    first = cache.solve(lh, noise=noise.cuda())
+    _check(first, ref, CFG.latent_dim, "ragged cached")
+    for rep in range(2):
+        again = cache.solve(lh, noise=noise.cuda())
+        assert torch.equal(again, first), f"repeat {rep}"

@@ -87,7 +87,10 @@ GEMM_CASES = [(1, 64, 64, 3), (37, 128, 256, 2), (300, 1024, 1024, -1), (700, 10
               # tile 9 (4 waves, AGPR accumulators, BK 32 x 5 stages): K steps 1, 2, 3, 4, 5 exercise the
               # guarded prologue / tail paths, the larger ones the unrolled steady state
               (1500, 4096, 1024, 9), (3001, 1024, 4096, 9), (700, 512, 32, 9), (333, 256, 64, 9),
-              (37, 256, 96, 9), (300, 768, 128, 9), (513, 256, 160, 9), (2000, 1024, 2048, 9)]
+              (37, 256, 96, 9), (300, 768, 128, 9), (513, 256, 160, 9), (2000, 1024, 2048, 9),
+              # tiles 10 / 11 (128-row blocks, 32 / 64 columns): decode-sized batches, and past 128 rows
+              (68, 1024, 4096, 10), (1, 1024, 1024, 10), (97, 32, 192, 10), (200, 512, 1024, 10),
+              (128, 3072, 1024, 11), (33, 128, 640, 11), (300, 256, 128, 11)]
 
 
 @pytest.mark.parametrize("M,N,K,tile", GEMM_CASES)
@@ -303,7 +306,10 @@ def test_full_size_nfe4_solve():
                                             (36937, 1024, 1024, 2, 4), (36937, 1024, 3072, 8, 0),
                                             (9000, 1024, 1024, 2, 1),
                                             (20000, 1024, 4096, 0, 4), (3000, 2048, 256, 3, 4),
-                                            (700, 1024, 256, 3, 0)])
+                                            (700, 1024, 256, 3, 0),
+                                            # the cached solve's decode-sized GEMMs on the 128-row tiles
+                                            (68, 4096, 1024, 10, 4), (68, 1024, 4096, 10, 1), (68, 1024, 1024, 10, 0),
+                                            (68, 1024, 3072, 11, 0), (100, 4096, 256, 10, 4), (128, 2048, 512, 11, 4)])
 def test_gemm_ksplit_matches_whole_tiles(M, K, N, tile, epi):
     """bf16 GEMM with the K-split workspace vs without (float32 sums in a
     different order: f32 output to 1e-5 relative, bf16 output to one ulp)."""

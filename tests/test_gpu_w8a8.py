@@ -75,7 +75,7 @@ def test_int32_accumulators_match_int_mm(M, K, N):
     assert torch.equal(acc, ref)
 
 
-@pytest.mark.parametrize("tile", [0, 1, 2, 3, 5, 7, 8, 9])
+@pytest.mark.parametrize("tile", [0, 1, 2, 3, 5, 7, 8, 9, 10, 11])
 def test_int32_all_tiles(tile):
     from nanovllm_dots_amd.int8 import gemm_w8a8
     M, K, N = 700, 1024, 1024
@@ -135,7 +135,8 @@ def _split_ws():
 
 
 @pytest.mark.parametrize("M,K,N,tile", [(36937, 4096, 1024, 8), (36937, 1024, 4096, 8), (20000, 4096, 1024, 0),
-                                        (3000, 2048, 256, 3), (36937, 4096, 1024, 9), (36937, 1024, 4096, 9)])
+                                        (3000, 2048, 256, 3), (36937, 4096, 1024, 9), (36937, 1024, 4096, 9),
+                                        (68, 4096, 1024, 10), (68, 1024, 3072, 11), (100, 2048, 256, 10)])
 def test_int32_ksplit_exact(M, K, N, tile):
     """K-split of the last partial tile round: int32 partial sums add exactly."""
     from nanovllm_dots_amd import _lib
