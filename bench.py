@@ -272,7 +272,7 @@ def power_bench(reps: int = 20):
     return res
 
 
-def kvcache_bench(head, cfg, reps: int = 10):
+def kvcache_bench(head, cfg, reps: int = 10, n: int = 4, patches: int = 600):
     """Long-audio cached solve: 4 streams, each with a cached prefix of 600 prior
     patches x 16 rows + 512 context rows (the last of them is the active block's
     hidden row), full 12-block DiT, NFE=4. Returns timings, xRT and the decode
@@ -280,7 +280,7 @@ def kvcache_bench(head, cfg, reps: int = 10):
     import numpy as np
     import torch
     from nanovllm_dots_amd import HipFMCache
-    n, rows = 4, 600 * 16 + 512
+    rows = patches * 16 + 512
     L = rows - 1
     H = cfg.hidden
     rs = np.random.RandomState(5)

@@ -29,13 +29,20 @@ COMMON = [
 ]
 
 
+# per-source flags. attention.hip: MFMA accumulators in VGPRs. Its kernels run at
+# most 3 waves per SIMD; the split-KV decode kernel (one wave per SIMD) would
+# otherwise keep scores and outputs in AGPRs and copy every one of them to VGPRs
+# for the softmax on every tile.
+EXTRA = {"attention.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+
+
 def sources() -> list[str]:
     return sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".hip"))
 
 
 def _compile(src: str, verbose: bool) -> str:
     obj = os.path.join(OUT_DIR, os.path.basename(src) + ".o")
-    cmd = [HIPCC, *COMMON, "-c", src, "-o", obj]
+    cmd = [HIPCC, *COMMON, *EXTRA.get(os.path.basename(src), []), "-c", src, "-o", obj]
     if verbose:
         print(" ".join(cmd), flush=True)
     r = subprocess.run(cmd, capture_output=True, text=True)

@@ -35,6 +35,7 @@
 // v_exp_f32 (results below 2^-126 flush to zero: such weights are below one
 // f32 ulp of the row's largest weight).
 #include <algorithm>
+#include <type_traits>
 
 #include "dfh_device.h"
 #include "dfh_kernels.h"
@@ -315,35 +316,43 @@ seq_attention_kernel(const uint16_t* __restrict__ qk, long ldqk, const uint16_t*
 // native/model.py:57-75). Group g = (sequence, head) is cut into chunks of
 // chunk_keys consecutive keys, one workgroup each, about one workgroup per CU
 // in all. Wave w of a chunk's workgroup takes the chunk's 64-key tiles
-// w, w + 4, ...: it stages each tile's K rows and V^T columns in its own LDS by
-// global->LDS DMA (whole 128-B lines, the swizzle and key-row permutation of
-// seq_attention_kernel), double-buffered, so the next tile streams in while the
-// wave scores this one with the online softmax of seq_attention_kernel (lazy
-// max refresh). Only the wave reads its tiles: no barrier inside the key loop.
-// The four waves' softmax states merge in LDS. A group of one chunk writes its
-// rows there; otherwise each chunk stores its partial (m in log2 units, l, O
-// of its <= 32 queries) and the last chunk of the group to finish merges the
-// group's partials and writes the rows. The chunks of a group are dealt to
-// workgroups with one value of blockIdx.x % 8, which the 8-XCD partition mode
-// places on one XCD: their partials meet in that XCD's L2. A chunk that finds
-// itself on another XCD (hardware register XCC_ID) publishes with an
+// w, w + NWV, ...: it stages each tile's K rows and V^T columns in its own LDS
+// by global->LDS DMA (whole 128-B lines, the swizzle and key-row permutation of
+// seq_attention_kernel) and scores it with the online softmax of
+// seq_attention_kernel (lazy max refresh); the next tile streams in while this
+// one is scored (a second stage, or the other wave of the SIMD). Only the wave
+// reads its tiles: no barrier inside the key loop. Only the sequence's last
+// tile is masked. The waves' softmax states merge in LDS. A group of one chunk
+// writes its rows there; otherwise each chunk stores its partial (m in log2
+// units, l, O of its <= 32 queries) and the last chunk of the group to finish
+// merges the group's partials (one round of loads for up to 8 chunks) and
+// writes the rows. The chunks of a group are dealt to workgroups with one
+// value of blockIdx.x % 8, which the 8-XCD partition mode places on one XCD:
+// their partials meet in that XCD's L2. A chunk that finds itself on another
+// XCD (hardware register XCC_ID) publishes with an
 // agent-scope release fence and marks the group's counter, and the merging
 // chunk of a marked group takes an agent-scope acquire fence. The last arriver
 // zeroes the counter for the next launch.
-constexpr int DWV = 4;                // waves per workgroup
 constexpr int PART = 32 * 66;         // per chunk: m[32], l[32], O[32][64]
 constexpr int kDecodeMaxChunks = 64;  // chunks per group (merge weights in LDS)
 constexpr int kWaveTile = 2 * BKV * HD;  // K tile then V^T tile, uint16_t elements
+// NWV waves per workgroup, NST stages per wave (tiles in flight per wave: NST - 1).
+// 8 waves of one stage (two waves per SIMD, 128 KB of tiles): while one wave of
+// a SIMD waits for its next tile the other computes.
+constexpr int kDecodeWaves = 8, kDecodeStages = 1;
 
-__global__ void __launch_bounds__(256)
+template <int NWV, int NST>
+__global__ void __launch_bounds__(64 * NWV)
 decode_attention_kernel(const uint16_t* __restrict__ qk, long ldqk, const uint16_t* __restrict__ vt,
                         long ld_vt, const AttnSeq* __restrict__ seqs, int heads, int n_groups, int n_chunks,
                         int chunk_keys, float scale_log2, float* __restrict__ part, unsigned* __restrict__ cnt,
                         uint16_t* __restrict__ out, long ldo, const float* __restrict__ rope_cos,
                         const float* __restrict__ rope_sin) {
-  // per wave two stages of (K tile [64 keys][64], V^T tile [64 d][64 keys]), 32 KB;
-  // after the key loop the wave's first 8.4 KB hold its O^T for the merge
-  __shared__ __attribute__((aligned(16))) uint16_t tiles[DWV * 2 * kWaveTile];
+  // per wave NST stages of (K tile [64 keys][64], V^T tile [64 d][64 keys]), 16 KB
+  // each; after the key loop the wave's first 8.4 KB hold its O^T for the merge
+  constexpr int DWV = NWV, NT = 64 * NWV;
+  static_assert(NST >= 1 && NST <= 4, "stages");
+  __shared__ __attribute__((aligned(16))) uint16_t tiles[DWV * NST * kWaveTile];
   __shared__ float Mw[DWV][32], Lw[DWV][32];
   __shared__ float Ws[kDecodeMaxChunks][32];
   __shared__ int s_flag;
@@ -358,29 +367,40 @@ decode_attention_kernel(const uint16_t* __restrict__ qk, long ldqk, const uint16
   const int k_hi = min(k_lo + chunk_keys, kv);
   const int nc = min((kv + chunk_keys - 1) / chunk_keys, n_chunks);  // chunks of this group
   const int H = heads * HD;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: tile and LDS bases in SGPRs
   const int l32 = lane & 31, hi = lane >> 5;
   const int nq = sq.q_end - sq.q_begin;
   const int n_t = (k_hi - k_lo + BKV - 1) / BKV;                 // tiles of the chunk
   const int nw = n_t > wave ? (n_t - wave + DWV - 1) / DWV : 0;  // this wave's tiles
-  uint16_t* st0 = tiles + wave * 2 * kWaveTile;
-  uint16_t* st1 = st0 + kWaveTile;
+  uint16_t* st0 = tiles + wave * NST * kWaveTile;
   const uint16_t* kbase = qk + (long)sq.kv_row0 * ldqk + H + h * HD;
   const uint16_t* vbase = vt + (long)(h * HD) * ld_vt + sq.vt_col0;
   // DMA of the wave's tile i (keys k_lo + (wave + 4i) * 64 + [0, 64)) into a stage:
   // load j fills tile rows [8j, 8j + 8): lane -> row 8j + lane/8, slot lane%8,
-  // which holds source chunk (lane%8) ^ swz(row). K rows past kv_len repeat the
-  // last key (masked below); V^T columns past it are finite (zeroed slack)
+  // which holds source chunk (lane%8) ^ swz(row); swz(row) = ((row >> 1) & 7)
+  // takes one value per lane for even j and another for odd j. Addresses are a
+  // uniform base per (tile, j) plus a per-lane byte offset that never changes.
+  // Tiles start at multiples of 64 keys of the sequence, and the caller's key
+  // space (a cache region) comes in whole 64-key tiles: rows and columns past
+  // kv_len stay inside it and hold finite values (K scores there are masked,
+  // their P is zero).
+  const uint32_t lr = lane >> 3;
+  const uint32_t k_off0 = (lr * (uint32_t)ldqk + (uint32_t)(((lane & 7) ^ ((lr >> 1) & 7)) * 8)) * 2u;
+  const uint32_t k_off1 = (lr * (uint32_t)ldqk + (uint32_t)(((lane & 7) ^ (((lr >> 1) + 4) & 7)) * 8)) * 2u;
+  const uint32_t v_off0 = (lr * (uint32_t)ld_vt + (uint32_t)(((lane & 7) ^ ((lr >> 1) & 7)) * 8)) * 2u;
+  const uint32_t v_off1 = (lr * (uint32_t)ld_vt + (uint32_t)(((lane & 7) ^ (((lr >> 1) + 4) & 7)) * 8)) * 2u;
   auto dma = [&](uint16_t* stage, int i) {
     const int key0 = k_lo + (wave + DWV * i) * BKV;
+    const char* kt = reinterpret_cast<const char*>(kbase + (long)key0 * ldqk);
+    const char* vtt = reinterpret_cast<const char*>(vbase + key0);
 #pragma unroll
     for (int jj = 0; jj < 8; ++jj) {
-      const int r = jj * 8 + (lane >> 3);
-      const int c = (lane & 7) ^ ((r >> 1) & 7);
-      const int key = min(key0 + r, kv - 1);
-      __builtin_amdgcn_global_load_lds(DFH_GPTR(kbase + (long)key * ldqk + c * 8),
+      const char* kj = kt + (long)jj * 8 * ldqk * 2;
+      const char* vj = vtt + (long)jj * 8 * ld_vt * 2;
+      __builtin_amdgcn_global_load_lds(DFH_GPTR(kj + ((jj & 1) ? k_off1 : k_off0)),
                                        DFH_LPTR(stage + jj * 8 * HD), 16, 0, 0);
-      __builtin_amdgcn_global_load_lds(DFH_GPTR(vbase + (long)r * ld_vt + key0 + c * 8),
+      __builtin_amdgcn_global_load_lds(DFH_GPTR(vj + ((jj & 1) ? v_off1 : v_off0)),
                                        DFH_LPTR(stage + BKV * HD + jj * 8 * BKV), 16, 0, 0);
     }
   };
@@ -402,7 +422,7 @@ decode_attention_kernel(const uint16_t* __restrict__ qk, long ldqk, const uint16
   float m_run = -INFINITY, l_run = 0.f;
   const float thr = kRescaleLog2 / scale_log2;  // in raw score units
 
-  auto compute = [&](const uint16_t* Ks, const uint16_t* Vs, int k0) {
+  auto compute = [&](auto masked, const uint16_t* Ks, const uint16_t* Vs, int k0) {
     floatx16 s[2];
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
@@ -415,7 +435,7 @@ decode_attention_kernel(const uint16_t* __restrict__ qk, long ldqk, const uint16
       }
     }
     // accumulator v of block kb holds key k0 + kb*32 + 16*(v/8) + 8*hi + v%8
-    if (k0 + BKV > kv) {  // wave-uniform: the sequence's last tile
+    if constexpr (decltype(masked)::value) {  // the sequence's last tile
       const int rel = kv - k0 - 8 * hi;
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
@@ -468,22 +488,32 @@ decode_attention_kernel(const uint16_t* __restrict__ qk, long ldqk, const uint16
       }
   };
 
-  // Tile i sits in stage i % 2. At the top of step i the wave waits for tile i
-  // (its only outstanding DMA) and for its LDS reads of tile i - 1, then starts
-  // tile i + 1 into the stage tile i - 1 used.
-  for (int i = 0; i < nw; i += 2) {
-    wait_vm_lgkm0<0>();
-    if (i + 1 < nw) dma(st1, i + 1);
-    compute(st0, st0 + BKV * HD, k_lo + (wave + DWV * i) * BKV);
-    if (i + 1 >= nw) break;
-    wait_vm_lgkm0<0>();
-    if (i + 2 < nw) dma(st0, i + 2);
-    compute(st1, st1 + BKV * HD, k_lo + (wave + DWV * (i + 1)) * BKV);
+  // Tile i sits in stage i % NST; tiles 0 .. NST - 2 go out first. At the top of
+  // step i the wave waits for tile i (the tiles after it, at most NST - 2 of
+  // them, may stay in flight: 16 DMA instructions each, completing in order) and
+  // for its LDS reads of tile i - 1, then starts tile i + NST - 1 into the stage
+  // tile i - 1 used. One stage: tile i + 1 starts once tile i's LDS reads are
+  // done, and the other waves of the SIMD compute meanwhile.
+  for (int i = 1; i < NST - 1 && i < nw; ++i) dma(st0 + i * kWaveTile, i);
+  for (int i = 0, si = 0; i < nw; ++i, si = si + 1 == NST ? 0 : si + 1) {
+    const int ahead = min(NST - 2, nw - 1 - i);
+    if (ahead <= 0) wait_vm_lgkm0<0>();
+    else if (ahead == 1) wait_vm_lgkm0<16>();
+    else wait_vm_lgkm0<32>();
+    if (NST > 1 && i + NST - 1 < nw) dma(st0 + (si == 0 ? NST - 1 : si - 1) * kWaveTile, i + NST - 1);
+    uint16_t* sb = st0 + si * kWaveTile;
+    const int k0 = k_lo + (wave + DWV * i) * BKV;
+    if (k0 + BKV <= kv) compute(std::false_type{}, sb, sb + BKV * HD, k0);
+    else compute(std::true_type{}, sb, sb + BKV * HD, k0);
+    if (NST == 1 && i + 1 < nw) {
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the tile's LDS reads are done
+      dma(st0, i + 1);
+    }
   }
   wait_vm_lgkm0<0>();  // (a wave without tiles) nothing outstanding into its stages
   // O^T[d][q] in lanes: q = l32, d = db*32 + 8*(v/4) + 4*hi + v%4; the wave's own stage space
   float (*Ow)[33] = reinterpret_cast<float (*)[33]>(st0);
-  static_assert(sizeof(float) * HD * 33 <= sizeof(uint16_t) * 2 * kWaveTile, "merge space");
+  static_assert(sizeof(float) * HD * 33 <= sizeof(uint16_t) * NST * kWaveTile, "merge space");
 #pragma unroll
   for (int db = 0; db < 2; ++db)
 #pragma unroll
@@ -494,7 +524,7 @@ decode_attention_kernel(const uint16_t* __restrict__ qk, long ldqk, const uint16
     Lw[wave][l32] = l_tot;
   }
   __syncthreads();
-  auto ow = [&](int w) { return reinterpret_cast<const float (*)[33]>(tiles + w * 2 * kWaveTile); };
+  auto ow = [&](int w) { return reinterpret_cast<const float (*)[33]>(tiles + w * NST * kWaveTile); };
   // merge of the four waves for query q: max M, weight of wave w = exp2(m_w - M)
   auto wave_merge = [&](int q, float& M, float (&wt)[DWV]) {
     M = -INFINITY;
@@ -504,7 +534,7 @@ decode_attention_kernel(const uint16_t* __restrict__ qk, long ldqk, const uint16
     for (int w = 0; w < DWV; ++w) wt[w] = Mw[w][q] != -INFINITY ? __builtin_amdgcn_exp2f(Mw[w][q] - M) : 0.f;
   };
   if (nc == 1) {  // the group's only chunk: normalised rows straight out
-    for (int e = tid; e < nq * (HD / 2); e += 256) {
+    for (int e = tid; e < nq * (HD / 2); e += NT) {
       const int q = e / (HD / 2), d = 2 * (e % (HD / 2));
       float M, wt[DWV];
       wave_merge(q, M, wt);
@@ -533,7 +563,7 @@ decode_attention_kernel(const uint16_t* __restrict__ qk, long ldqk, const uint16
       pp[tid] = M;
       pp[32 + tid] = L;
     }
-    for (int e = tid; e < nq * HD; e += 256) {
+    for (int e = tid; e < nq * HD; e += NT) {
       const int q = e / HD, d = e % HD;
       float M, wt[DWV];
       wave_merge(q, M, wt);
@@ -557,32 +587,87 @@ decode_attention_kernel(const uint16_t* __restrict__ qk, long ldqk, const uint16
   if (s_flag == 2) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
   asm volatile("" ::: "memory");
   if (tid == 0) cnt[g] = 0u;  // ready for the next launch
-  // Last chunk in: per query the chunk weights exp2(m_c - M) / L go to LDS, then
-  // every thread adds two output columns of one query over the chunks in chunk order.
+  // Last chunk in. Up to CB chunks: each thread loads m, l and its two O columns
+  // of every chunk at once (one round trip; the 32 threads of a query share the
+  // m / l addresses), then M = max m_c, L = sum l_c exp2(m_c - M) and
+  // O = sum exp2(m_c - M) / L * O_c, each in chunk order. More chunks: the chunk
+  // weights go through LDS first.
+  constexpr int CB = 8;
+  if (nc <= CB) {
+    for (int e = tid; e < nq * (HD / 2); e += NT) {
+      const int q = e / (HD / 2), d = 2 * (e % (HD / 2));
+      float mc[CB], lc[CB];
+      float2 x[CB];
+#pragma unroll
+      for (int b = 0; b < CB; ++b) {
+        const float* pc = pg + (long)min(b, nc - 1) * PART;
+        mc[b] = pc[q];
+        lc[b] = pc[32 + q];
+        x[b] = *reinterpret_cast<const float2*>(pc + 64 + q * HD + d);
+      }
+      float M = -INFINITY;
+#pragma unroll
+      for (int b = 0; b < CB; ++b)
+        if (b < nc) M = fmaxf(M, mc[b]);
+      float L = 0.f;
+#pragma unroll
+      for (int b = 0; b < CB; ++b)
+        if (b < nc && mc[b] != -INFINITY) L += lc[b] * __builtin_amdgcn_exp2f(mc[b] - M);
+      const float inv = 1.0f / L;
+      float o0 = 0.f, o1 = 0.f;
+#pragma unroll
+      for (int b = 0; b < CB; ++b)
+        if (b < nc) {
+          const float w = mc[b] != -INFINITY ? __builtin_amdgcn_exp2f(mc[b] - M) * inv : 0.f;
+          o0 += w * x[b].x;
+          o1 += w * x[b].y;
+        }
+      *reinterpret_cast<uint32_t*>(out + (long)(sq.out_row0 + sq.q_begin + q) * ldo + h * HD + d) = pack2(o0, o1);
+    }
+    return;
+  }
+  // every chunk's m and l to LDS (one load per thread and pair; Ow is dead: the
+  // second stage of wave 0), per query the chunk weights, then the O columns
+  // over the chunks in chunk order, CB chunks' loads in flight together
+  float (*Mc)[32] = reinterpret_cast<float (*)[32]>(tiles + kWaveTile);
+  float (*Lc)[32] = Mc + kDecodeMaxChunks;
+  static_assert(2 * kDecodeMaxChunks * 32 * sizeof(float) <= kWaveTile * sizeof(uint16_t), "m / l space");
+  for (int e = tid; e < nc * 32; e += NT) {
+    const int c = e >> 5, q = e & 31;
+    Mc[c][q] = pg[(long)c * PART + q];
+    Lc[c][q] = pg[(long)c * PART + 32 + q];
+  }
+  __syncthreads();
   if (tid < nq) {
     float M = -INFINITY;
-    for (int c = 0; c < nc; ++c) M = fmaxf(M, pg[(long)c * PART + tid]);
+    for (int c = 0; c < nc; ++c) M = fmaxf(M, Mc[c][tid]);
     float L = 0.f;
     for (int c = 0; c < nc; ++c) {
-      const float mc = pg[(long)c * PART + tid];
-      if (mc != -INFINITY) L += pg[(long)c * PART + 32 + tid] * __builtin_amdgcn_exp2f(mc - M);
+      const float mc = Mc[c][tid];
+      if (mc != -INFINITY) L += Lc[c][tid] * __builtin_amdgcn_exp2f(mc - M);
     }
     const float inv = 1.0f / L;
     for (int c = 0; c < nc; ++c) {
-      const float mc = pg[(long)c * PART + tid];
+      const float mc = Mc[c][tid];
       Ws[c][tid] = mc != -INFINITY ? __builtin_amdgcn_exp2f(mc - M) * inv : 0.f;
     }
   }
   __syncthreads();
-  for (int e = tid; e < nq * (HD / 2); e += 256) {
+  for (int e = tid; e < nq * (HD / 2); e += NT) {
     const int q = e / (HD / 2), d = 2 * (e % (HD / 2));
     const float* po = pg + 64 + q * HD + d;
     float o0 = 0.f, o1 = 0.f;
-    for (int c = 0; c < nc; ++c) {
-      const float w = Ws[c][q];
-      const float2 x = *reinterpret_cast<const float2*>(po + (long)c * PART);
-      o0 += w * x.x;
-      o1 += w * x.y;
+    for (int c0 = 0; c0 < nc; c0 += CB) {
+      float2 x[CB];
+#pragma unroll
+      for (int b = 0; b < CB; ++b) x[b] = *reinterpret_cast<const float2*>(po + (long)min(c0 + b, nc - 1) * PART);
+#pragma unroll
+      for (int b = 0; b < CB; ++b)
+        if (c0 + b < nc) {
+          const float w = Ws[c0 + b][q];
+          o0 += w * x[b].x;
+          o1 += w * x[b].y;
+        }
     }
     *reinterpret_cast<uint32_t*>(out + (long)(sq.out_row0 + sq.q_begin + q) * ldo + h * HD + d) = pack2(o0, o1);
   }
@@ -617,21 +702,22 @@ hipError_t decode_attention(const uint16_t* qk, long ldqk, const uint16_t* vt, l
   const DecodeSplit sp = decode_split(n_seq, heads, max_kv);
   const long groups8 = ((long)n_seq * heads + NXCD - 1) / NXCD * NXCD;
   if (groups8 * sp.n_chunks > 0x7fffffffL) return hipErrorInvalidValue;
-  dfh_launch(decode_attention_kernel, dim3((unsigned)(groups8 * sp.n_chunks)), dim3(256), 0, s, qk, ldqk, vt,
+  dfh_launch(decode_attention_kernel<kDecodeWaves, kDecodeStages>, dim3((unsigned)(groups8 * sp.n_chunks)),
+             dim3(64 * kDecodeWaves), 0, s, qk, ldqk, vt,
              ld_vt, seqs, heads, n_seq * heads, sp.n_chunks, sp.chunk_keys, scale_log2, part, counters, out, ldo,
              rope_cos, rope_sin);
   return hipGetLastError();
 }
 
 DecodeSplit decode_split(int n_seq, int heads, int max_kv) {
-  // about one workgroup per CU (each holds 128 KB of LDS), chunks of whole
-  // 256-key rounds (one 64-key tile per wave)
+  // about one workgroup per CU (each holds 128 KB of tiles), chunks of whole
+  // rounds of one 64-key tile per wave
   const long groups = (long)n_seq * heads;
   int want = (int)(cu_count() / (groups > 0 ? groups : 1));
-  const int rounds = (max_kv + DWV * BKV - 1) / (DWV * BKV);
+  const int rounds = (max_kv + kDecodeWaves * BKV - 1) / (kDecodeWaves * BKV);
   want = std::max(1, std::min(std::min(want, rounds), kDecodeMaxChunks));
   DecodeSplit sp;
-  sp.chunk_keys = (rounds + want - 1) / want * (DWV * BKV);
+  sp.chunk_keys = (rounds + want - 1) / want * (kDecodeWaves * BKV);
   sp.n_chunks = (max_kv + sp.chunk_keys - 1) / sp.chunk_keys;
   return sp;
 }

@@ -136,6 +136,8 @@ hipError_t seq_attention(const uint16_t* qk, long ldqk, const uint16_t* vt, long
 // chunk partials in `part` and writes the rows. part holds
 // n_seq * heads * n_chunks * 32 * 66 floats (n_chunks <= ceil(max_kv / 256));
 // counters holds n_seq * heads zeroed words and is left zeroed by every launch.
+// Keys are read in whole 64-key tiles: the q|k rows and V^T columns of a
+// sequence up to kv_len rounded up to 64 must be readable and finite.
 struct DecodeSplit {
   int n_chunks = 1, chunk_keys = 256;
 };
