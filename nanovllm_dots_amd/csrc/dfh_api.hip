@@ -1118,7 +1118,14 @@ struct DfhKVCache {
   DevBuf lens, counts, offs, seqs, c_rows, row_req, row_pos, vt_col, patch_rows, lh_rows, part, part_cnt, z;
   long table_rows = 0;
   std::vector<int> lens_host;
-  int* pinned = nullptr;  // 2n+1 ints staged for uploads
+  // extend's uploads (counts, prefix sums: 2n + 2 ints) go through a ring of
+  // pinned slots; a slot is rewritten once the event recorded after its copies
+  // has completed, kPinnedSlots calls later, so the host does not wait on the stream
+  static constexpr int kPinnedSlots = 8;
+  int* pinned = nullptr;
+  hipEvent_t pinned_ev[kPinnedSlots] = {};
+  bool pinned_used[kPinnedSlots] = {};
+  int pinned_next = 0;
 };
 
 namespace {
@@ -1247,6 +1254,7 @@ int cache_alloc(DfhHandle* h, int n, int cap, int S, DfhKVCache** out) {
                       &c->part_cnt, &c->z};
     for (DevBuf* b : bufs) if (b->p) (void)hipFree(b->p);
     if (c->pinned) (void)hipHostFree(c->pinned);
+    for (hipEvent_t ev : c->pinned_ev) if (ev) (void)hipEventDestroy(ev);
     delete c;
     return fail("kv cache allocation: %s", hipGetErrorString(e));
   };
@@ -1268,7 +1276,10 @@ int cache_alloc(DfhHandle* h, int n, int cap, int S, DfhKVCache** out) {
   if (e == hipSuccess) e = dev_alloc(c->part_cnt, (size_t)n * cf.heads * 4);
   if (e == hipSuccess) e = hipMemset(c->part_cnt.p, 0, (size_t)n * cf.heads * 4);
   if (e == hipSuccess) e = dev_alloc(c->z, (size_t)n * cf.patch * cf.latent_dim * 2);
-  if (e == hipSuccess) e = hipHostMalloc(reinterpret_cast<void**>(&c->pinned), (2 * n + 2) * sizeof(int));
+  if (e == hipSuccess)
+    e = hipHostMalloc(reinterpret_cast<void**>(&c->pinned), (size_t)DfhKVCache::kPinnedSlots * (2 * n + 2) * sizeof(int));
+  for (int k = 0; k < DfhKVCache::kPinnedSlots && e == hipSuccess; ++k)
+    e = hipEventCreateWithFlags(&c->pinned_ev[k], hipEventDisableTiming);
   if (e != hipSuccess) return bail(e);
   c->lens_host.assign(n, 0);
   *out = c;
@@ -1308,6 +1319,7 @@ int dfh_kvcache_destroy(DfhKVCache* c) {
                     &c->vt_col, &c->patch_rows, &c->lh_rows, &c->part, &c->part_cnt, &c->z};
   for (DevBuf* b : bufs) if (b->p) (void)hipFree(b->p);
   if (c->pinned) (void)hipHostFree(c->pinned);
+  for (hipEvent_t ev : c->pinned_ev) if (ev) (void)hipEventDestroy(ev);
   delete c;
   return 0;
 }
@@ -1340,13 +1352,18 @@ int dfh_kvcache_extend(DfhKVCache* c, const void* rows, int m_max, const int* co
     max_count = counts[i] > max_count ? counts[i] : max_count;
   }
   if (Mtot == 0) return 0;
-  // stage counts and their exclusive prefix sums (the pinned buffer is free once the stream is idle)
-  DFH_CHECK(hipStreamSynchronize(s));
+  // stage counts and their exclusive prefix sums in the next pinned slot
+  const int slot = c->pinned_next;
+  c->pinned_next = (slot + 1) % DfhKVCache::kPinnedSlots;
+  if (c->pinned_used[slot]) DFH_CHECK(hipEventSynchronize(c->pinned_ev[slot]));
+  int* pin = c->pinned + (size_t)slot * (2 * c->n + 2);
   int acc = 0;
-  for (int i = 0; i < c->n; ++i) { c->pinned[i] = counts[i]; c->pinned[c->n + 1 + i] = acc; acc += counts[i]; }
-  c->pinned[2 * c->n + 1] = acc;
-  DFH_CHECK(hipMemcpyAsync(c->counts.p, c->pinned, (size_t)c->n * 4, hipMemcpyHostToDevice, s));
-  DFH_CHECK(hipMemcpyAsync(c->offs.p, c->pinned + c->n + 1, (size_t)(c->n + 1) * 4, hipMemcpyHostToDevice, s));
+  for (int i = 0; i < c->n; ++i) { pin[i] = counts[i]; pin[c->n + 1 + i] = acc; acc += counts[i]; }
+  pin[2 * c->n + 1] = acc;
+  DFH_CHECK(hipMemcpyAsync(c->counts.p, pin, (size_t)c->n * 4, hipMemcpyHostToDevice, s));
+  DFH_CHECK(hipMemcpyAsync(c->offs.p, pin + c->n + 1, (size_t)(c->n + 1) * 4, hipMemcpyHostToDevice, s));
+  DFH_CHECK(hipEventRecord(c->pinned_ev[slot], s));
+  c->pinned_used[slot] = true;
   TimeVals tv{}, dtv{};
   for (int k = 0; k < c->S; ++k) { tv.v[k] = t_grid[k]; dtv.v[k] = dt_grid[k]; }
   const int H = c->h->cfg.hidden;

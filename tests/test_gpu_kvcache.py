@@ -163,3 +163,25 @@ def test_decode_chunks_ragged_streams_and_repeated_solves():
     for rep in range(2):
         again = cache.solve(lh, noise=noise.cuda())
         assert torch.equal(again, first), f"repeat {rep}"
+
+
+def test_many_back_to_back_extends():
+    """Twelve extends in a row with no host wait between them (their uploads
+    cycle through the ring of pinned staging slots and reuse them) agree with
+    one extend of the same rows."""
+    from nanovllm_dots_amd import HipFMCache
+    head, _ = _head(CFG, 4)
+    lens, hist, noise = R.synthetic_requests(2, 150, 200, CFG, seed=13)
+    prefix = [h[:-1] for h in hist]
+    lh = torch.stack([h[-1] for h in hist]).cuda()
+    whole = HipFMCache(head, 2, 256, 4)
+    whole.extend(_pad(prefix, CFG.hidden).cuda(), [p.shape[0] for p in prefix])
+    ref = whole.solve(lh, noise=noise.cuda())
+    inc = HipFMCache(head, 2, 256, 4)
+    cuts = [np.linspace(0, p.shape[0], 13).astype(int) for p in prefix]
+    for k in range(12):
+        parts = [p[c[k]:c[k + 1]] for p, c in zip(prefix, cuts)]
+        inc.extend(_pad(parts, CFG.hidden).cuda(), [q.shape[0] for q in parts])
+    assert inc.lengths == [p.shape[0] for p in prefix]
+    got = inc.solve(lh, noise=noise.cuda())
+    _check(got, ref, CFG.latent_dim, "12 extends vs one")
