@@ -198,6 +198,12 @@ typedef struct DfhInt8Weights {
   const DfhInt8Linear *qkv, *o, *fc1, *fc2;     /* host arrays [n_blocks]; qkv [3H, H] */
 } DfhInt8Weights;
 int dfh_set_int8(DfhHandle* h, int enable, const DfhInt8Weights* w, void* stream);
+/* int8 mode: the LayerNorm + modulate in front of QKV and fc1 also writes its
+ * rows per-token quantised (default on), bit-identical to quantising its bf16
+ * output in a pass of its own (off). No reference counterpart: in
+ * D/int8_dit.py:57-58 the quantisation is part of Int8DynamicLinear.forward;
+ * fusing it is a scheduling choice of this library. */
+int dfh_set_ln_quant(DfhHandle* h, int enable);
 
 /* dfh_gemm_bf16 with a device workspace (ws, ws_bytes) for the K-split of the
  * last partial round of tiles (see dfh_set_ksplit); too small or NULL: no split.

@@ -107,6 +107,7 @@ struct DfhHandle {
   DevBuf splitws;  // K-split: tile counters, then a 256x256 f32 partial tile per resident workgroup
   DevBuf attq;     // attention work list: item count, then one AttnItem per 128-query tile
   bool ksplit = true;
+  bool ln_quant = true;  // int8 mode: LayerNorm+modulate also quantises the next linear's input rows
   bool latent_tail = true;  // solve: the last block's attention / O / MLP on the latent rows only
 
   // W8A8 mode (Int8DynamicLinear / quantize_dit_, int8_dit.py:34-85): every DiT
@@ -180,15 +181,20 @@ int reserve_q8(DfhHandle* h, long rows, hipStream_t s) {
 // A linear layer: the bf16 GEMM, or in int8 mode with an int8 weight q, the
 // input rows quantised per token (bit-exact with int8_dit.py:57-58) and the i8
 // GEMM with the epilogue that dequantises first ((acc * s_x) * s_w) + b.
-hipError_t lin(DfhHandle* h, int pc, const GemmArgs& a, int epi, const Q8& q, hipStream_t s, int tile = -1) {
+// a_ready: the input rows are already quantised in h->aq / h->asx (by the
+// LayerNorm+modulate that produced them, ln_q8); a.A is then not read.
+hipError_t lin(DfhHandle* h, int pc, const GemmArgs& a, int epi, const Q8& q, hipStream_t s, int tile = -1,
+               bool a_ready = false) {
   if (!h->int8 || !q.w) return gemm(h, pc, a, epi, s, tile);
   if (a.M > h->aq_rows || (long)a.K > (h->cfg.ffn > h->cfg.hidden ? h->cfg.ffn : h->cfg.hidden))
     return hipErrorInvalidValue;  // reserve_q8 sizes the rows beforehand
   int8_t* aq = P<int8_t>(h->aq);
   float* sx = P<float>(h->asx);
-  prof_arm(h, PC_QUANT);
-  hipError_t e = quant_rows_bf16(a.A, a.lda, aq, a.K, sx, a.M, a.K, s, a.M_dev);
-  if (e != hipSuccess) return e;
+  if (!a_ready) {
+    prof_arm(h, PC_QUANT);
+    hipError_t e = quant_rows_bf16(a.A, a.lda, aq, a.K, sx, a.M, a.K, s, a.M_dev);
+    if (e != hipSuccess) return e;
+  }
   GemmArgs b = a;
   b.A = reinterpret_cast<const uint16_t*>(aq); b.lda = a.K;   // bytes
   b.B = reinterpret_cast<const uint16_t*>(q.w); b.ldb = a.K;
@@ -202,6 +208,22 @@ hipError_t lin(DfhHandle* h, int pc, const GemmArgs& a, int epi, const Q8& q, hi
     b.ws_elems = (long)(h->splitws.bytes / 4);
   }
   return gemm_i8(b, epi8, s, tile);
+}
+
+// LayerNorm + modulate of the rows that feed the linear with int8 weight q. In
+// int8 mode (and with the fused quantiser on) the rows also leave quantised in
+// h->aq / h->asx for lin(..., a_ready = true); keep_bf16 = false skips the bf16
+// rows when nothing else reads them. Returns whether the rows are quantised.
+bool ln_q8(DfhHandle* h, const uint16_t* x, uint16_t* out, const uint16_t* shift, const uint16_t* scale,
+           long ldm, const int* row_req, int Mup, const int* Md, const Q8& q, bool keep_bf16, hipStream_t s,
+           hipError_t* err) {
+  const DfhConfig& c = h->cfg;
+  const int H = c.hidden;
+  const bool fuse = h->int8 && q.w && h->ln_quant && Mup <= h->aq_rows;
+  prof_arm(h, PC_LN);
+  *err = ln_modulate(x, H, (fuse && !keep_bf16) ? nullptr : out, H, shift, scale, ldm, row_req, nullptr, Mup, Md,
+                     H, c.ln_eps, s, fuse ? P<int8_t>(h->aq) : nullptr, H, fuse ? P<float>(h->asx) : nullptr);
+  return fuse;
 }
 
 // Tile shape per GEMM role (indices of gemm_bf16's configurations), chosen from
@@ -438,9 +460,12 @@ int run_blocks(DfhHandle* h, const Pass& p, hipStream_t s) {
     const uint16_t* ml = mod + (long)l * 6 * H;  // shift_a, scale_a, gate_a, shift_f, scale_f, gate_f
     // block 0 of a pass with hoisted input rows reads them; its first gate-residual writes h->x
     const uint16_t* xin = (l == 0 && p.x0) ? p.x0 : P<uint16_t>(h->x);
-    prof_arm(h, PC_LN);
-    DFH_CHECK(ln_modulate(xin, H, P<uint16_t>(h->hbuf), H, ml + 0 * H, ml + 1 * H, ldm,
-                          row_req, nullptr, Mup, Md, H, c.ln_eps, s));
+    // the last block of a latent-tail pass also gathers bf16 LayerNorm rows
+    const bool last_special = (p.latent_tail || p.kv_only_last) && l == c.n_blocks - 1;
+    hipError_t lerr;
+    const bool q1 = ln_q8(h, xin, P<uint16_t>(h->hbuf), ml + 0 * H, ml + 1 * H, ldm, row_req, Mup, Md,
+                          h->int8 ? h->qkv_q[l] : Q8{}, last_special, s, &lerr);
+    DFH_CHECK(lerr);
     GemmArgs q = linear_args(P<uint16_t>(h->hbuf), H, h->qkv_w[l], h->qkv_b[l], p.qk[l], p.ldqk, Mup, Md,
                              3 * H, H);
     q.hidden = H; q.head_dim = c.head_dim;
@@ -463,11 +488,12 @@ int run_blocks(DfhHandle* h, const Pass& p, hipStream_t s) {
       kv.B = h->qkv_w[l] + (long)H * H; kv.N = 2 * H; kv.col0 = H;
       Q8 kv8 = h->int8 ? h->qkv_q[l] : Q8{};
       if (kv8.w) kv8.w += (long)H * H;  // scales stay indexed by the q|k|v column
-      DFH_CHECK(lin(h, p.kv_only_last ? PC_QKV : PC_TAIL, kv, EPI_QKV, kv8, s, tile_for(Mup, 2 * H, H, kRoleQKV)));
+      DFH_CHECK(lin(h, p.kv_only_last ? PC_QKV : PC_TAIL, kv, EPI_QKV, kv8, s, tile_for(Mup, 2 * H, H, kRoleQKV),
+                    q1));
       if (p.kv_only_last) break;
       return run_latent_tail(h, p, l, ml, ldm, q, xin, s);
     }
-    DFH_CHECK(lin(h, PC_QKV, q, EPI_QKV, h->int8 ? h->qkv_q[l] : Q8{}, s, tile_for(Mup, 3 * H, H, kRoleQKV)));
+    DFH_CHECK(lin(h, PC_QKV, q, EPI_QKV, h->int8 ? h->qkv_q[l] : Q8{}, s, tile_for(Mup, 3 * H, H, kRoleQKV), q1));
     prof_arm(h, PC_ATTN);
     if (p.decode)
       DFH_CHECK(decode_attention(p.qk[l], p.ldqk, p.vt[l], p.ld_vt, P<uint16_t>(h->attn), H, p.seqs, p.n_seq,
@@ -480,12 +506,12 @@ int run_blocks(DfhHandle* h, const Pass& p, hipStream_t s) {
     o.gate = ml + 2 * H; o.ld_gate = ldm; o.row_req = row_req;
     if (xin != P<uint16_t>(h->x)) { o.res = xin; o.ld_res = H; }
     DFH_CHECK(lin(h, PC_O, o, EPI_GATE_RES, h->int8 ? h->o_q[l] : Q8{}, s, tile_for(Mup, H, H, kRoleNarrow)));
-    prof_arm(h, PC_LN);
-    DFH_CHECK(ln_modulate(P<uint16_t>(h->x), H, P<uint16_t>(h->hbuf), H, ml + 3 * H, ml + 4 * H, ldm,
-                          row_req, nullptr, Mup, Md, H, c.ln_eps, s));
+    const bool q2 = ln_q8(h, P<uint16_t>(h->x), P<uint16_t>(h->hbuf), ml + 3 * H, ml + 4 * H, ldm, row_req, Mup,
+                          Md, h->int8 ? h->fc1_q[l] : Q8{}, false, s, &lerr);
+    DFH_CHECK(lerr);
     DFH_CHECK(lin(h, PC_FC1, linear_args(P<uint16_t>(h->hbuf), H, h->fc1_w[l], h->fc1_b[l],
                                          P<uint16_t>(h->ff), F, Mup, Md, F, H), EPI_GELU,
-                  h->int8 ? h->fc1_q[l] : Q8{}, s, tile_for(Mup, F, H, kRoleWide)));
+                  h->int8 ? h->fc1_q[l] : Q8{}, s, tile_for(Mup, F, H, kRoleWide), q2));
     GemmArgs f2 = linear_args(P<uint16_t>(h->ff), F, h->fc2_w[l], h->fc2_b[l], P<uint16_t>(h->x), H,
                               Mup, Md, H, F);
     f2.gate = ml + 5 * H; f2.ld_gate = ldm; f2.row_req = row_req;
@@ -908,6 +934,12 @@ int dfh_input_status(DfhHandle* h, int* flags, void* stream) {
 int dfh_set_ksplit(DfhHandle* h, int enable) {
   if (!h) return fail("null handle");
   h->ksplit = enable != 0;
+  return 0;
+}
+
+int dfh_set_ln_quant(DfhHandle* h, int enable) {
+  if (!h) return fail("null handle");
+  h->ln_quant = enable != 0;
   return 0;
 }
 

@@ -89,10 +89,13 @@ hipError_t quant_weight_f32(const uint16_t* w, int8_t* q, float* scale, int N, i
 // Row kernels -------------------------------------------------------------------
 // LayerNorm (no affine, fp32 stats) + adaLN modulate:
 //   out[m] = bf16( LN(x[m]) * bf16(1 + scale[req]) + shift[req] )
+// q (with sx, ldq >= H): the bf16 rows also leave per-token quantised, as
+// quant_rows_bf16 would quantise them (bit-identical); out may then be null.
 hipError_t ln_modulate(const uint16_t* x, long ldx, uint16_t* out, long ldo,
                        const uint16_t* shift, const uint16_t* scale, long ld_mod,
                        const int* row_req, const int* row_map, int rows_upper, const int* M_dev,
-                       int H, float eps, hipStream_t s);
+                       int H, float eps, hipStream_t s, int8_t* q = nullptr, long ldq = 0,
+                       float* sx = nullptr);
 
 // One attention sequence (device array element). Rows index the q|k buffer
 // ([rows, 2H]: q in columns [0, H), k in [H, 2H)); V^T is [H, ld_vt].

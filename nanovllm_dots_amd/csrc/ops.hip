@@ -12,12 +12,18 @@ namespace {
 // DiTBlock.forward / FinalLayer.forward (nanovllm_dots/models/dots/native/dit.py:
 // 99-105, 60-63) under bf16 autocast: LN in fp32, (1 + scale) rounded to bf16,
 // fp32 product and sum, one rounding to bf16 at the consumer's input.
-template <int VPT>  // values per lane = H / 64, multiple of 4
+//
+// QO: the row also leaves as the int8 input of the next W8A8 linear (q, sx),
+// exactly what the per-token quantiser makes of the bf16 row
+// (D/int8_dit.py:57-58; the operations of quant_rows_kernel); out may then be
+// null (no bf16 row stored).
+template <int VPT, bool QO>  // values per lane = H / 64, multiple of 4
 __global__ void __launch_bounds__(256)
 ln_modulate_kernel(const uint16_t* __restrict__ x, long ldx, uint16_t* __restrict__ out, long ldo,
                    const uint16_t* __restrict__ shift, const uint16_t* __restrict__ scale,
                    long ld_mod, const int* __restrict__ row_req, const int* __restrict__ row_map,
-                   int rows, const int* __restrict__ M_dev, int H, float eps) {
+                   int rows, const int* __restrict__ M_dev, int H, float eps, int8_t* __restrict__ q,
+                   long ldq, float* __restrict__ sx) {
   // 16-B accesses (8 values) where the row splits evenly, else 8-B
   constexpr int W = VPT % 8 == 0 ? 8 : 4;
   constexpr int NJ = VPT / W;
@@ -63,7 +69,6 @@ ln_modulate_kernel(const uint16_t* __restrict__ x, long ldx, uint16_t* __restric
   }
   const float var = wave_sum(s2) / (float)H;
   const float rstd = rsqrtf(var + eps);
-  uint16_t* op = out + (long)r * ldo;
   float y[VPT];
 #pragma unroll
   for (int t = 0; t < VPT; ++t) {
@@ -71,15 +76,50 @@ ln_modulate_kernel(const uint16_t* __restrict__ x, long ldx, uint16_t* __restric
     const float onep = rbf(1.0f + sc[t]);
     y[t] = add_rn(mul_rn(ln, onep), sh[t]);
   }
+  if (!QO || out) {
+    uint16_t* op = out + (long)r * ldo;
 #pragma unroll
-  for (int j = 0; j < NJ; ++j) {
-    const int col = (j * 64 + lane) * W;
-    if constexpr (W == 8) {
-      const uint2 lo = pack4(y[8 * j], y[8 * j + 1], y[8 * j + 2], y[8 * j + 3]);
-      const uint2 hi2 = pack4(y[8 * j + 4], y[8 * j + 5], y[8 * j + 6], y[8 * j + 7]);
-      *reinterpret_cast<uint4*>(op + col) = make_uint4(lo.x, lo.y, hi2.x, hi2.y);
-    } else {
-      *reinterpret_cast<uint2*>(op + col) = pack4(y[4 * j], y[4 * j + 1], y[4 * j + 2], y[4 * j + 3]);
+    for (int j = 0; j < NJ; ++j) {
+      const int col = (j * 64 + lane) * W;
+      if constexpr (W == 8) {
+        const uint2 lo = pack4(y[8 * j], y[8 * j + 1], y[8 * j + 2], y[8 * j + 3]);
+        const uint2 hi2 = pack4(y[8 * j + 4], y[8 * j + 5], y[8 * j + 6], y[8 * j + 7]);
+        *reinterpret_cast<uint4*>(op + col) = make_uint4(lo.x, lo.y, hi2.x, hi2.y);
+      } else {
+        *reinterpret_cast<uint2*>(op + col) = pack4(y[4 * j], y[4 * j + 1], y[4 * j + 2], y[4 * j + 3]);
+      }
+    }
+  }
+  if constexpr (QO) {
+    // the bf16 row's absolute maximum, s = bf16(amax / 127) (at least bf16(1e-8)),
+    // then bf16(x / s) from y = RN(1 / s) with one FMA correction, rounded, clamped
+    float amax = 0.f;
+#pragma unroll
+    for (int t = 0; t < VPT; ++t) {
+      y[t] = rbf(y[t]);
+      amax = fmaxf(amax, fabsf(y[t]));
+    }
+    amax = wave_max(amax);
+    float sr = rbf(__fdiv_rn(amax, 127.0f));
+    sr = fmaxf(sr, rbf(1e-8f));
+    if (lane == 0) sx[r] = sr;
+    const float yi = __fdiv_rn(1.0f, sr);
+    int8_t* qp = q + (long)r * ldq;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const int col = (j * 64 + lane) * W;
+      uint32_t packed[W / 4] = {};
+#pragma unroll
+      for (int t = 0; t < W; ++t) {
+        const float xv = y[W * j + t];
+        const float q0 = mul_rn(xv, yi);
+        const float q1 = __builtin_fmaf(__builtin_fmaf(-sr, q0, xv), yi, q0);  // RN(x / s)
+        float vq = rintf(rbf(q1));
+        vq = fminf(fmaxf(vq, -127.f), 127.f);
+        packed[t >> 2] |= ((uint32_t)(uint8_t)(int8_t)(int)vq) << (8 * (t & 3));
+      }
+      if constexpr (W == 8) *reinterpret_cast<uint2*>(qp + col) = make_uint2(packed[0], packed[1]);
+      else *reinterpret_cast<uint32_t*>(qp + col) = packed[0];
     }
   }
 }
@@ -392,15 +432,21 @@ hipError_t cache_advance(int* lens, const int* counts, int n, hipStream_t s) {
 
 hipError_t ln_modulate(const uint16_t* x, long ldx, uint16_t* out, long ldo, const uint16_t* shift,
                        const uint16_t* scale, long ld_mod, const int* row_req, const int* row_map,
-                       int rows_upper, const int* M_dev, int H, float eps, hipStream_t s) {
+                       int rows_upper, const int* M_dev, int H, float eps, hipStream_t s, int8_t* q, long ldq,
+                       float* sx) {
   if (rows_upper <= 0) return hipSuccess;
   if (H % 256 != 0) return hipErrorInvalidValue;
+  if (q ? (!sx || ldq < H || ldq % 8 != 0) : !out) return hipErrorInvalidValue;
   dim3 grid((rows_upper + 3) / 4), block(256);
   switch (H / 64) {
-#define DFH_LN(V)                                                                           \
-  case V:                                                                                  \
-    dfh_launch(ln_modulate_kernel<V>, grid, block, 0, s, x, ldx, out, ldo, shift, \
-                       scale, ld_mod, row_req, row_map, rows_upper, M_dev, H, eps);        \
+#define DFH_LN(V)                                                                                         \
+  case V:                                                                                                \
+    if (q)                                                                                               \
+      dfh_launch(ln_modulate_kernel<V, true>, grid, block, 0, s, x, ldx, out, ldo, shift, scale, ld_mod, \
+                 row_req, row_map, rows_upper, M_dev, H, eps, q, ldq, sx);                               \
+    else                                                                                                 \
+      dfh_launch(ln_modulate_kernel<V, false>, grid, block, 0, s, x, ldx, out, ldo, shift, scale, ld_mod,\
+                 row_req, row_map, rows_upper, M_dev, H, eps, q, ldq, sx);                               \
     break;
     DFH_LN(4)
     DFH_LN(8)

@@ -359,6 +359,11 @@ class HipFMHead:
         """K-split of each GEMM's last partial round of tiles (on by default)."""
         _lib.check(self.lib.dfh_set_ksplit(self.handle, int(enable)), "dfh_set_ksplit")
 
+    def set_ln_quant(self, enable: bool) -> None:
+        """int8 mode: quantise QKV's and fc1's input rows inside LayerNorm+modulate
+        (on by default; bit-identical to the separate quantiser pass)."""
+        _lib.check(self.lib.dfh_set_ln_quant(self.handle, int(enable)), "dfh_set_ln_quant")
+
     def set_latent_tail(self, enable: bool) -> None:
         """Last block of a solve on the latent rows only (on by default): the
         caller keeps v[:, -P:] (batched_fm.py:122-124), so only those rows'

@@ -86,3 +86,33 @@ def test_quantized_module_weights_are_taken_as_they_are():
         HipFMHead(FMSpec.of(cfg), partial, device="cuda")
     head_ref.close()
     head_q.close()
+
+
+def test_fused_layernorm_quantiser_is_bit_identical():
+    """QKV's and fc1's input rows quantised inside LayerNorm+modulate against the
+    separate per-token quantiser pass over the bf16 rows: the same int8 rows and
+    scales, so the same latents bit for bit (solve with its latent tail, and
+    the cached solve's prime and decode passes)."""
+    from nanovllm_dots_amd import FMSpec, HipFMCache, HipFMHead
+    cfg = SMALL
+    W = R.random_dit_weights(cfg, 5)
+    head = HipFMHead(FMSpec.of(cfg), W, device="cuda", int8=True)
+    lens, hist, noise = R.synthetic_requests(3, 25, 160, cfg, 6, regime="bf16")
+    print(f"fused ln quantiser: lens {lens}", flush=True)
+    outs = []
+    for fused in (True, False):
+        head.set_ln_quant(fused)
+        solve = _solve(head, cfg, hist, noise)
+        cache = HipFMCache(head, 3, max(lens) + 24, 4)
+        prefix = [h[:-1] for h in hist]
+        rows = torch.zeros(3, max(p.shape[0] for p in prefix), cfg.hidden)
+        for i, p in enumerate(prefix):
+            rows[i, :p.shape[0]] = p
+        cache.extend(rows.cuda(), [p.shape[0] for p in prefix])
+        cached = cache.solve(torch.stack([h[-1] for h in hist]).cuda(), noise=noise.cuda())
+        cache.close()
+        outs.append((solve, cached))
+    head.set_ln_quant(True)
+    assert torch.equal(outs[0][0], outs[1][0])
+    assert torch.equal(outs[0][1], outs[1][1])
+    head.close()
