@@ -213,8 +213,10 @@ seq_attention_kernel(const uint16_t* __restrict__ qk, long ldqk, const uint16_t*
   const float thr = kRescaleLog2 / scale_log2;  // in raw score units
   const int krow = key_perm(l32);
 
-  auto compute = [&](const uint16_t* Ks, const uint16_t* Vs, int k0) {
-    if (k0 >= wave_kmax) return;  // wave-uniform
+  // masked: the tile crosses some lane's visible-key limit (wave-uniform test
+  // at the call site; two copies of the tile code, so unmasked tiles carry no
+  // per-score compare and select)
+  auto compute = [&](auto masked, const uint16_t* Ks, const uint16_t* Vs, int k0) {
     floatx16 s[2];
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
@@ -227,7 +229,7 @@ seq_attention_kernel(const uint16_t* __restrict__ qk, long ldqk, const uint16_t*
       }
     }
     // accumulator v of block kb holds key k0 + kb*32 + 16*(v/8) + 8*hi + v%8
-    if (k0 + BKV > wave_kall) {
+    if constexpr (decltype(masked)::value) {
       const int rel = lim - k0 - 8 * hi;
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
@@ -280,17 +282,22 @@ seq_attention_kernel(const uint16_t* __restrict__ qk, long ldqk, const uint16_t*
       }
   };
 
+  auto tile = [&](const uint16_t* Ks, const uint16_t* Vs, int k0) {
+    if (k0 >= wave_kmax) return;  // wave-uniform: no key of the tile is visible to the wave
+    if (k0 + BKV > wave_kall) compute(std::true_type{}, Ks, Vs, k0);
+    else compute(std::false_type{}, Ks, Vs, k0);
+  };
   dma(K0, V0, 0);
   for (int t = 0; t < ntiles; t += 2) {
     wait_vm_lgkm0<0>();
     __builtin_amdgcn_s_barrier();
     if (t + 1 < ntiles) dma(K1, V1, (t + 1) * BKV);
-    compute(K0, V0, t * BKV);
+    tile(K0, V0, t * BKV);
     if (t + 1 >= ntiles) break;
     wait_vm_lgkm0<0>();
     __builtin_amdgcn_s_barrier();
     if (t + 2 < ntiles) dma(K0, V0, (t + 2) * BKV);
-    compute(K1, V1, (t + 1) * BKV);
+    tile(K1, V1, (t + 1) * BKV);
   }
 
   const float l_tot = l_run + swap_halves(l_run);
