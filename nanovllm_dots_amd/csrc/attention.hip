@@ -287,17 +287,15 @@ seq_attention_kernel(const uint16_t* __restrict__ qk, long ldqk, const uint16_t*
     if (k0 + BKV > wave_kall) compute(std::true_type{}, Ks, Vs, k0);
     else compute(std::false_type{}, Ks, Vs, k0);
   };
+  // one tile per iteration (stage t % 2): a single copy of the tile code keeps
+  // the kernel at 123 VGPRs, four workgroups per CU
   dma(K0, V0, 0);
-  for (int t = 0; t < ntiles; t += 2) {
+  for (int t = 0; t < ntiles; ++t) {
     wait_vm_lgkm0<0>();
     __builtin_amdgcn_s_barrier();
-    if (t + 1 < ntiles) dma(K1, V1, (t + 1) * BKV);
-    tile(K0, V0, t * BKV);
-    if (t + 1 >= ntiles) break;
-    wait_vm_lgkm0<0>();
-    __builtin_amdgcn_s_barrier();
-    if (t + 2 < ntiles) dma(K0, V0, (t + 2) * BKV);
-    tile(K1, V1, (t + 1) * BKV);
+    const bool odd = t & 1;
+    if (t + 1 < ntiles) dma(odd ? K0 : K1, odd ? V0 : V1, (t + 1) * BKV);
+    tile(odd ? K1 : K0, odd ? V1 : V0, t * BKV);
   }
 
   const float l_tot = l_run + swap_halves(l_run);
