@@ -46,7 +46,7 @@ namespace {
 //           per MFMA than SCHED 1; under random bf16 operands both run into the
 //           chip's power limit at about the same rate, and SCHED 1 has the
 //           smaller per-tile overhead, so production shapes use SCHED 1.
-template <int BM_, int BN_, int BK_, int ST_, int WM_, int WN_, int SCHED_ = 0>
+template <int BM_, int BN_, int BK_, int ST_, int WM_, int WN_, int SCHED_ = 0, int MAXSPLIT_ = 0>
 struct Cfg {
   static constexpr int BM = BM_, BN = BN_, BK = BK_, ST = ST_, WM = WM_, WN = WN_, SCHED = SCHED_;
   static constexpr int HD = SCHED == 1;  // the DMA of step j issued by half j % 2
@@ -63,7 +63,7 @@ struct Cfg {
   static constexpr int AJ = BM / RPR, BJ = BN / RPR;
   static constexpr int LPS = AJ + BJ;               // DMA instructions per wave per K step
   // K pieces per leftover tile at most (its last piece reads the others' partial sums)
-  static constexpr int MAX_SPLIT = SCHED == 2 ? 2 : 64;
+  static constexpr int MAX_SPLIT = MAXSPLIT_ ? MAXSPLIT_ : SCHED == 2 ? 2 : 64;
   static constexpr int LDS_BYTES = ST * (BM + BN) * BK * 2;
   // two workgroups per CU when both fit in LDS (then <= 256 registers per lane)
   static constexpr int WG_PER_CU = (NW <= 4 && 2 * LDS_BYTES <= 160 * 1024) ? 2 : 1;
@@ -1144,9 +1144,12 @@ using T7 = Cfg<128, 128, 32, 4, 2, 2>;  // 4 waves, 4 stages of BK 32, 64 KB: tw
 using T8 = Cfg<256, 256, 64, 2, 2, 4, 1>;  // T0 with the DMA of a step issued by one half
 using T9 = Cfg<256, 256, 32, 5, 2, 2, 2>;  // 4 waves, 128x128 per wave (AGPRs), DMA spread over the MFMAs, 160 KB
 // at most 128 rows (a decode-sized batch): one row block, narrow column blocks
-// and K pieces spread the weights over the whole chip; two workgroups per CU
-using T10 = Cfg<128, 32, 64, 4, 4, 1>;  // 4 waves, 32x32 per wave, 80 KB
-using T11 = Cfg<128, 64, 64, 3, 4, 1>;  // 4 waves, 32x64 per wave (RoPE pairs of the QKV epilogue), 72 KB
+// and K pieces spread the weights over the whole chip; two workgroups per CU.
+// At most 8 pieces per tile: at 68 rows, K = 4096 runs faster as 8 pieces of 8
+// K steps than as 16 of 4 (the last piece's sum and epilogue cost per piece),
+// while K = 1024 is fastest as 4 pieces of 4.
+using T10 = Cfg<128, 32, 64, 4, 4, 1, 0, 8>;  // 4 waves, 32x32 per wave, 80 KB
+using T11 = Cfg<128, 64, 64, 3, 4, 1, 0, 8>;  // 4 waves, 32x64 per wave (RoPE pairs of the QKV epilogue), 72 KB
 constexpr int kNumTiles = 12;
 const int kTileBM[kNumTiles] = {T0::BM, T1::BM, T2::BM, T3::BM, T4::BM,  T5::BM,
                                 T6::BM, T7::BM, T8::BM, T9::BM, T10::BM, T11::BM};
