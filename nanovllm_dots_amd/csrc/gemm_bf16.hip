@@ -46,7 +46,8 @@ namespace {
 //           per MFMA than SCHED 1; under random bf16 operands both run into the
 //           chip's power limit at about the same rate, and SCHED 1 has the
 //           smaller per-tile overhead, so production shapes use SCHED 1.
-template <int BM_, int BN_, int BK_, int ST_, int WM_, int WN_, int SCHED_ = 0, int MAXSPLIT_ = 0>
+template <int BM_, int BN_, int BK_, int ST_, int WM_, int WN_, int SCHED_ = 0, int MAXSPLIT_ = 0,
+          int MINSTEPS_ = 8>
 struct Cfg {
   static constexpr int BM = BM_, BN = BN_, BK = BK_, ST = ST_, WM = WM_, WN = WN_, SCHED = SCHED_;
   static constexpr int HD = SCHED == 1;  // the DMA of step j issued by half j % 2
@@ -64,6 +65,8 @@ struct Cfg {
   static constexpr int LPS = AJ + BJ;               // DMA instructions per wave per K step
   // K pieces per leftover tile at most (its last piece reads the others' partial sums)
   static constexpr int MAX_SPLIT = MAXSPLIT_ ? MAXSPLIT_ : SCHED == 2 ? 2 : 64;
+  // K steps per piece at least: the last piece's sum and epilogue cost per piece
+  static constexpr int MIN_SPLIT_STEPS = MINSTEPS_;
   static constexpr int LDS_BYTES = ST * (BM + BN) * BK * 2;
   // two workgroups per CU when both fit in LDS (then <= 256 registers per lane)
   static constexpr int WG_PER_CU = (NW <= 4 && 2 * LDS_BYTES <= 160 * 1024) ? 2 : 1;
@@ -537,21 +540,20 @@ __device__ __forceinline__ void run_epilogue(const GemmArgs& a, ACC (&acc)[C::RN
 
 // K-split of an XCD's last round: chunk_x tiles over per_xcd workgroups leave
 // tail = chunk_x mod per_xcd tiles for a partial round. Cut each of them into
-// split = per_xcd / tail K pieces (at least kMinSplitSteps K steps each) so the
+// split = per_xcd / tail K pieces (at least min_steps K steps each) so the
 // round takes 1/split of a tile instead of a whole one.
-constexpr int kMinSplitSteps = 4;
 // workspace layout: kSplitCounters 32-bit tile counters (index xcd * per_xcd +
 // leftover tile; at a fixed place for every tile shape, zero between calls),
 // then one BM x BN float32 partial tile per workgroup
 constexpr long kSplitCounters = 4096;
-__device__ __forceinline__ void split_plan(int chunk_x, int per_xcd, int KT, int max_split, int& full_x,
-                                           int& split) {
+__device__ __forceinline__ void split_plan(int chunk_x, int per_xcd, int KT, int max_split, int min_steps,
+                                           int& full_x, int& split) {
   full_x = chunk_x;
   split = 1;
   const int rounds = chunk_x / per_xcd, tail = chunk_x - rounds * per_xcd;
   if (tail == 0) return;
   int sp = per_xcd / tail;
-  if (sp > KT / kMinSplitSteps) sp = KT / kMinSplitSteps;
+  if (sp > KT / min_steps) sp = KT / min_steps;
   if (sp > max_split) sp = max_split;
   if (sp < 2) return;
   full_x = rounds * per_xcd;
@@ -613,7 +615,7 @@ gemm_mfma_kernel(GemmArgs a) {
   int chunk_x = total - xcd * chunk;
   chunk_x = chunk_x < 0 ? 0 : (chunk_x > chunk ? chunk : chunk_x);
   int full_x = chunk_x, split = 1;
-  if (a.ws != nullptr) split_plan(chunk_x, per_xcd, K / BK, C::MAX_SPLIT, full_x, split);
+  if (a.ws != nullptr) split_plan(chunk_x, per_xcd, K / BK, C::MAX_SPLIT, C::MIN_SPLIT_STEPS, full_x, split);
   auto tile_at = [&](int jt) { return jt < full_x ? xcd * chunk + jt : -1; };
   // Grouped order: the per_xcd tiles an XCD runs at once cover GM row blocks x
   // per_xcd/GM column blocks (row block fastest), so each A row block and W
@@ -1145,11 +1147,11 @@ using T8 = Cfg<256, 256, 64, 2, 2, 4, 1>;  // T0 with the DMA of a step issued b
 using T9 = Cfg<256, 256, 32, 5, 2, 2, 2>;  // 4 waves, 128x128 per wave (AGPRs), DMA spread over the MFMAs, 160 KB
 // at most 128 rows (a decode-sized batch): one row block, narrow column blocks
 // and K pieces spread the weights over the whole chip; two workgroups per CU.
-// At most 8 pieces per tile: at 68 rows, K = 4096 runs faster as 8 pieces of 8
-// K steps than as 16 of 4 (the last piece's sum and epilogue cost per piece),
-// while K = 1024 is fastest as 4 pieces of 4.
-using T10 = Cfg<128, 32, 64, 4, 4, 1, 0, 8>;  // 4 waves, 32x32 per wave, 80 KB
-using T11 = Cfg<128, 64, 64, 3, 4, 1, 0, 8>;  // 4 waves, 32x64 per wave (RoPE pairs of the QKV epilogue), 72 KB
+// At most 8 pieces of at least 4 K steps per tile: at 68 rows, K = 4096 runs
+// faster as 8 pieces of 8 K steps than as 16 of 4 (the last piece's sum and
+// epilogue cost per piece), while K = 1024 is fastest as 4 pieces of 4.
+using T10 = Cfg<128, 32, 64, 4, 4, 1, 0, 8, 4>;  // 4 waves, 32x32 per wave, 80 KB
+using T11 = Cfg<128, 64, 64, 3, 4, 1, 0, 8, 4>;  // 4 waves, 32x64 per wave (RoPE pairs of the QKV epilogue), 72 KB
 constexpr int kNumTiles = 12;
 const int kTileBM[kNumTiles] = {T0::BM, T1::BM, T2::BM, T3::BM, T4::BM,  T5::BM,
                                 T6::BM, T7::BM, T8::BM, T9::BM, T10::BM, T11::BM};
