@@ -1305,8 +1305,7 @@ int cache_alloc(DfhHandle* h, int n, int cap, int S, DfhKVCache** out) {
   if (e == hipSuccess) e = dev_alloc(c->patch_rows, (size_t)n * cf.patch * 4);
   if (e == hipSuccess) e = dev_alloc(c->lh_rows, (size_t)n * 4);
   if (e == hipSuccess) e = dev_alloc(c->part, (size_t)n * cf.heads * n_chunks * 32 * 66 * 4);
-  if (e == hipSuccess) e = dev_alloc(c->part_cnt, (size_t)n * cf.heads * 4);
-  if (e == hipSuccess) e = hipMemset(c->part_cnt.p, 0, (size_t)n * cf.heads * 4);
+  if (e == hipSuccess) e = dev_alloc(c->part_cnt, (size_t)n * cf.heads * 4);  // zero-filled
   if (e == hipSuccess) e = dev_alloc(c->z, (size_t)n * cf.patch * cf.latent_dim * 2);
   if (e == hipSuccess)
     e = hipHostMalloc(reinterpret_cast<void**>(&c->pinned), (size_t)DfhKVCache::kPinnedSlots * (2 * n + 2) * sizeof(int));
