@@ -283,10 +283,11 @@ def kvcache_bench(head, cfg, reps: int = 10, n: int = 4, patches: int = 600):
     rows = patches * 16 + 512
     L = rows - 1
     H = cfg.hidden
+    n_ext = 4  # per-patch extends timed after the solves (16 rows per stream each)
     rs = np.random.RandomState(5)
-    hist = torch.from_numpy(rs.standard_normal((n, rows, H)).astype(np.float32)).bfloat16().cuda()
+    hist = torch.from_numpy(rs.standard_normal((n, rows + 16 * n_ext, H)).astype(np.float32)).bfloat16().cuda()
     noise = torch.from_numpy(rs.standard_normal((n, cfg.patch, cfg.latent_dim)).astype(np.float32)).bfloat16().cuda()
-    cache = HipFMCache(head, n, rows + cfg.patch + 8, 4)
+    cache = HipFMCache(head, n, rows + 16 * n_ext + cfg.patch + 8, 4)
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
@@ -313,6 +314,13 @@ def kvcache_bench(head, cfg, reps: int = 10, n: int = 4, patches: int = 600):
     prof = head.profile_read()
     head.profile(False)
     assert torch.isfinite(out.float()).all()
+    # the engine's per-patch step besides the solve: extend every stream by one patch (16 rows)
+    e0.record()
+    for k in range(n_ext):
+        cache.extend(hist[:, L + 1 + 16 * k: L + 1 + 16 * (k + 1)], [16] * n)
+    e1.record()
+    torch.cuda.synchronize()
+    ext_ms = e0.elapsed_time(e1) / n_ext
     attn_ms, attn_n = prof["attention"]
     kv_bytes_launch = n * 2 * (L + 1 + cfg.patch) * H * 2       # one layer's K and V, all streams
     gbps = kv_bytes_launch / (attn_ms / attn_n * 1e-3) / 1e9
@@ -323,7 +331,8 @@ def kvcache_bench(head, cfg, reps: int = 10, n: int = 4, patches: int = 600):
            "decode_attn_us_per_layer": round(attn_ms / attn_n * 1e3, 2),
            "decode_attn_GBps": round(gbps, 1), "decode_attn_frac_hbm": round(gbps / PEAK_HBM_GBS, 4),
            "prime_ms": round(prime_ms, 2), "prime_tflops": round(prime_flops / (prime_ms * 1e-3) / 1e12, 1),
-           "kernel_ms_per_solve": {k: round(v[0] / reps, 3) for k, v in prof.items() if v[1]}}
+           "kernel_ms_per_solve": {k: round(v[0] / reps, 3) for k, v in prof.items() if v[1]},
+           "extend_16_rows_ms": round(ext_ms, 3)}
     log(f"kvcache: {res}")
     cache.close()
     return res
