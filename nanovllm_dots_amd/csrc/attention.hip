@@ -49,6 +49,8 @@ constexpr int BKV = 64;    // keys per tile
 constexpr int HD = 64;     // head dim
 constexpr int NXCD = 8;
 constexpr float kRescaleLog2 = 8.0f;  // lazy max refresh threshold (log2 units)
+// buffer resource word 3 for gfx9-family raw (stride 0) buffers: 32-bit data format
+constexpr int kBufferFlags = 0x00020000;
 
 typedef float floatx8 __attribute__((ext_vector_type(8)));
 
@@ -186,21 +188,36 @@ seq_attention_kernel(const uint16_t* __restrict__ qk, long ldqk, const uint16_t*
   }
   if (rope_cos) rope_q(qf, qc, hi, rope_cos, rope_sin);  // uniform
 
-  // DMA: wave w, load j covers tile rows [(4j + w) * 8, +8); lane -> row + lane/8, slot lane%8
+  // DMA: wave w, load j covers tile rows [(4j + w) * 8, +8); lane -> row + lane/8, slot lane%8.
+  // Buffer loads: a lane's byte offsets are the same for every tile. K rows
+  // through a resource that starts at the tile's first key and ends at key T:
+  // rows past the sequence arrive as zeros (their scores are masked). V^T
+  // columns at the tile's key offset (soffset); columns past T are read as
+  // they are (finite; their weights are zero).
   const int dma_r0 = wave * 8 + (lane >> 3);
   const int dma_c = lane & 7;
   const uint16_t* kbase = qk + (long)sq.kv_row0 * ldqk + H + h * HD;
-  const uint16_t* vbase = vt + (long)(h * HD) * ld_vt + sq.vt_col0;
+  uint32_t koff[2], voff[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int r = j * 32 + dma_r0;
+    const int c = dma_c ^ ((r >> 1) & 7);
+    koff[j] = ((uint32_t)r * (uint32_t)ldqk + (uint32_t)c * 8u) * 2u;
+    voff[j] = ((uint32_t)r * (uint32_t)ld_vt + (uint32_t)c * 8u) * 2u;
+  }
+  const __amdgpu_buffer_rsrc_t vres = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(vt + (long)(h * HD) * ld_vt + sq.vt_col0), (short)0, (int)((uint32_t)HD * (uint32_t)ld_vt * 2u),
+      kBufferFlags);
+  const int wave_u = __builtin_amdgcn_readfirstlane(wave);  // the LDS destinations (M0) in scalars
   auto dma = [&](uint16_t* kd, uint16_t* vd, int k0) {
+    const __amdgpu_buffer_rsrc_t kres = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(kbase + (long)k0 * ldqk), (short)0, (int)((uint32_t)(T - k0) * (uint32_t)ldqk * 2u), kBufferFlags);
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
-      const int r = j * 32 + dma_r0;
-      const int c = dma_c ^ ((r >> 1) & 7);
-      const int key = min(k0 + r, T - 1);
-      __builtin_amdgcn_global_load_lds(DFH_GPTR(kbase + (long)key * ldqk + c * 8),
-                                       DFH_LPTR(kd + (j * 32 + wave * 8) * 64), 16, 0, 0);
-      __builtin_amdgcn_global_load_lds(DFH_GPTR(vbase + (long)r * ld_vt + k0 + c * 8),
-                                       DFH_LPTR(vd + (j * 32 + wave * 8) * 64), 16, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(kres, DFH_LPTR(kd + (j * 32 + wave_u * 8) * 64), 16, koff[j], 0, 0,
+                                               0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(vres, DFH_LPTR(vd + (j * 32 + wave_u * 8) * 64), 16, voff[j], k0 * 2,
+                                               0, 0);
     }
   };
 
@@ -212,21 +229,36 @@ seq_attention_kernel(const uint16_t* __restrict__ qk, long ldqk, const uint16_t*
   float m_run = -INFINITY, l_run = 0.f;
   const float thr = kRescaleLog2 / scale_log2;  // in raw score units
   const int krow = key_perm(l32);
+  // per-lane byte offsets of the fragment reads within a stage (a tile's
+  // second 32-row block starts 4096 B on, with the same swizzle)
+  uint32_t krd[4], vrd[4];
+#pragma unroll
+  for (int kk = 0; kk < 4; ++kk) krd[kk] = (uint32_t)att_off(krow, 2 * kk + hi) * 2u;
+#pragma unroll
+  for (int c = 0; c < 4; ++c) vrd[c] = (uint32_t)att_off(l32, 2 * c + hi) * 2u;  // k-step (kb, half): c = 2kb + half
 
   // masked: the tile crosses some lane's visible-key limit (wave-uniform test
   // at the call site; two copies of the tile code, so unmasked tiles carry no
   // per-score compare and select)
+  // one 16-B fragment read per (lane address, block): the stage's base is added
+  // once per address, the block offset rides in the instruction
+  auto frag = [](uint32_t addr, int off) {
+    return *reinterpret_cast<const __attribute__((address_space(3))) bf16x8*>((uintptr_t)(addr + off));
+  };
   auto compute = [&](auto masked, const uint16_t* Ks, const uint16_t* Vs, int k0) {
+    const uint32_t kst = (uint32_t)(uintptr_t)DFH_LPTR(Ks), vst = (uint32_t)(uintptr_t)DFH_LPTR(Vs);
     floatx16 s[2];
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
+    for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
       for (int v = 0; v < 16; ++v) s[kb][v] = 0.f;
 #pragma unroll
-      for (int kk = 0; kk < 4; ++kk) {
-        const bf16x8 kf = *reinterpret_cast<const bf16x8*>(Ks + att_off(kb * 32 + krow, 2 * kk + hi));
-        s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[kk], s[kb], 0, 0, 0);
-      }
+    for (int kk = 0; kk < 4; ++kk) {
+      uint32_t ka = kst + krd[kk];
+      asm volatile("" : "+v"(ka));  // keeps the block offset out of the address sum
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+        s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(frag(ka, kb * 4096), qf[kk], s[kb], 0, 0, 0);
     }
     // accumulator v of block kb holds key k0 + kb*32 + 16*(v/8) + 8*hi + v%8
     if constexpr (decltype(masked)::value) {
@@ -273,12 +305,11 @@ seq_attention_kernel(const uint16_t* __restrict__ qk, long ldqk, const uint16_t*
 #pragma unroll
         for (int j = 0; j < 8; ++j) pv[j] = s[kb][8 * half + j];
         const bf16x8 pf = __builtin_convertvector(pv, bf16x8);
+        uint32_t va = vst + vrd[2 * kb + half];
+        asm volatile("" : "+v"(va));
 #pragma unroll
-        for (int db = 0; db < 2; ++db) {
-          const bf16x8 vf =
-              *reinterpret_cast<const bf16x8*>(Vs + att_off(db * 32 + l32, 4 * kb + 2 * half + hi));
-          o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf, o[db], 0, 0, 0);
-        }
+        for (int db = 0; db < 2; ++db)
+          o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(frag(va, db * 4096), pf, o[db], 0, 0, 0);
       }
   };
 
