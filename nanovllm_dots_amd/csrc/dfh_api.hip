@@ -123,6 +123,7 @@ struct DfhHandle {
 
   // profiling
   bool prof = false;
+  unsigned prof_mask = ~0u;  // classes whose launches carry events
   std::vector<hipEvent_t> ev_pool;
   std::vector<std::pair<int, int>> ev_used;  // (class, pool index of start)
   size_t ev_next = 0;
@@ -134,7 +135,7 @@ namespace {
 
 // arm dispatch-packet events for the next launch of class `pc`
 void prof_arm(DfhHandle* h, int pc) {
-  if (!h->prof) return;
+  if (!h->prof || !((h->prof_mask >> pc) & 1u)) return;
   if (h->ev_next + 2 > h->ev_pool.size()) return;  // pool full: drop the sample
   const int i = (int)h->ev_next;
   h->ev_next += 2;
@@ -956,6 +957,12 @@ int dfh_profile_enable(DfhHandle* h, int enable) {
     for (auto& ev : h->ev_pool) DFH_CHECK(hipEventCreate(&ev));
   }
   h->prof = enable != 0;
+  return 0;
+}
+
+int dfh_profile_classes(DfhHandle* h, unsigned mask) {
+  if (!h) return fail("null handle");
+  h->prof_mask = mask;
   return 0;
 }
 
