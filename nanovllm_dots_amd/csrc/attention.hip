@@ -190,10 +190,11 @@ seq_attention_kernel(const uint16_t* __restrict__ qk, long ldqk, const uint16_t*
 
   // DMA: wave w, load j covers tile rows [(4j + w) * 8, +8); lane -> row + lane/8, slot lane%8.
   // Buffer loads: a lane's byte offsets are the same for every tile. K rows
-  // through a resource that starts at the tile's first key and ends at key T:
-  // rows past the sequence arrive as zeros (their scores are masked). V^T
-  // columns at the tile's key offset (soffset); columns past T are read as
-  // they are (finite; their weights are zero).
+  // through a resource that starts at the tile's first key and ends at key
+  // min(T, first key + 64): rows past the sequence arrive as zeros (their
+  // scores are masked). V^T columns at the tile's key offset (soffset);
+  // columns past T are read as they are (finite; their weights are zero). The
+  // launcher keeps every byte offset below 2^31.
   const int dma_r0 = wave * 8 + (lane >> 3);
   const int dma_c = lane & 7;
   const uint16_t* kbase = qk + (long)sq.kv_row0 * ldqk + H + h * HD;
@@ -211,7 +212,8 @@ seq_attention_kernel(const uint16_t* __restrict__ qk, long ldqk, const uint16_t*
   const int wave_u = __builtin_amdgcn_readfirstlane(wave);  // the LDS destinations (M0) in scalars
   auto dma = [&](uint16_t* kd, uint16_t* vd, int k0) {
     const __amdgpu_buffer_rsrc_t kres = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)(kbase + (long)k0 * ldqk), (short)0, (int)((uint32_t)(T - k0) * (uint32_t)ldqk * 2u), kBufferFlags);
+        (void*)(kbase + (long)k0 * ldqk), (short)0, (int)((uint32_t)min(T - k0, BKV) * (uint32_t)ldqk * 2u),
+        kBufferFlags);
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       __builtin_amdgcn_raw_ptr_buffer_load_lds(kres, DFH_LPTR(kd + (j * 32 + wave_u * 8) * 64), 16, koff[j], 0, 0,
@@ -721,6 +723,9 @@ hipError_t seq_attention(const uint16_t* qk, long ldqk, const uint16_t* vt, long
                          long ldo, int heads, const void* list, long max_items, const float* rope_cos,
                          const float* rope_sin, hipStream_t s) {
   if (max_items <= 0) return hipSuccess;
+  // the kernel's buffer offsets are 32-bit: a tile's 64 q|k rows, a head's 64 V^T rows
+  if (ldqk <= 0 || ld_vt <= 0 || (long)BKV * ldqk * 2 >= (1L << 31) || (long)HD * ld_vt * 2 >= (1L << 31))
+    return hipErrorInvalidValue;
   const float scale_log2 = 0.125f * 1.4426950408889634f;  // head_dim^-0.5 * log2(e)
   const long grid = max_items * heads;
   if (grid > 0x7fffffffL) return hipErrorInvalidValue;
