@@ -190,6 +190,29 @@ def test_meanflow_solve_matches_oracle(name):
     _assert_vs_fp32(got, Wb, cfg, hist, g, noise, f"meanflow-{name}")
 
 
+def test_edge_lengths_and_a_long_request_match_fp32_oracle():
+    """Histories at the 64-key and 128-query tile edges (1, 63, 64, 65, 127,
+    128, 129 rows) and one long request (3,000 rows: 24 query tiles, a work-list
+    bucket of its own, 47 key tiles) in one batch, padded and varlen, against
+    the fp32 oracle's solve of the same requests."""
+    from nanovllm_dots_amd import HipMeanflow
+    cfg = VARIANTS["rope"]
+    head, Wb = _head(cfg, seed=21)
+    lens = [1, 63, 64, 65, 127, 128, 129, 3000]
+    rng = np.random.RandomState(21)
+    hist = [R.round_bf16(torch.from_numpy(rng.standard_normal((L, cfg.hidden)).astype(np.float32))) for L in lens]
+    noise = R.round_bf16(torch.from_numpy(
+        rng.standard_normal((len(lens), cfg.patch, cfg.latent_dim)).astype(np.float32)))
+    inp, _, pos, g = R.pack_fm_inputs(hist, cfg.patch, cfg.hidden)
+    print(f"edge lengths {lens}", flush=True)
+    mf = HipMeanflow(None, num_steps=4, dit=object(), head=head, strict=True)
+    got = mf(input_sequence=_cuda_bf16(inp), attn_mask=None, pos_ids=pos.cuda(), g_cond=_cuda_bf16(g),
+             noise=_cuda_bf16(noise))
+    _assert_vs_fp32(got, Wb, cfg, hist, g, noise, "edge lengths")
+    vl = head.solve_varlen([_cuda_bf16(h) for h in hist], lens, _cuda_bf16(g), _cuda_bf16(noise), 4, strict=True)
+    assert torch.equal(vl, got)
+
+
 def test_padding_transparency_bit_exact():
     """A ragged batch gives each request bit-identical latents to a solo run."""
     from nanovllm_dots_amd import HipMeanflow
