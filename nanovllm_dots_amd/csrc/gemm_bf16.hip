@@ -428,6 +428,127 @@ __device__ __forceinline__ void qkv_epilogue(const GemmArgs& a, ACC (&acc)[C::RN
   }
 }
 
+// QKV epilogue with a fixed number of stores per lane (bf16 operands; no
+// qk-norm, no output-row table). Every load comes before the first store: the
+// row tables of all row blocks and the bias at the start, block k+1's RoPE
+// factors before block k's stores, so no load waits for a store. The stores
+// go through buffer resources that drop rows at or past M instead of a row
+// branch, so a lane issues RM * RN * 4 of them on a q|k tile and
+// RM * RN * 16 on a V tile, and the next tile's first K step waits for its
+// prologue DMA only. Same values as qkv_epilogue. Returns 0 (q|k tile),
+// 1 (V tile) or 2 (qkv_epilogue ran: the next step waits for everything).
+template <class C>
+__device__ __forceinline__ int qkv_epilogue_fixed(const GemmArgs& a, floatx16 (&acc)[C::RN][C::RM], int m0,
+                                                  int n0, int M, int wm, int wn, int l32, int hi) {
+  const int H = a.hidden;
+  if (a.qk_norm || a.c_rows || (long)H * a.ld_vt * 2 >= 0x7fffffffL) {  // uniform
+    qkv_epilogue<C, false>(a, acc, m0, n0, M, wm, wn, l32, hi);
+    return 2;
+  }
+  const int nq = n0 + a.col0 + wn * C::WTN;  // this wave's first column within q|k|v (= column of C)
+  const int region = (n0 + a.col0) / H;      // 0 q, 1 k, 2 v (BN divides H)
+  int rt[C::RM];                             // per row block: V^T column (v) or position (q, k)
+#pragma unroll
+  for (int k = 0; k < C::RM; ++k) {
+    const int m = m0 + wm * C::WTM + k * 32 + l32;
+    const int mm = m < M ? m : M - 1;
+    rt[k] = region == 2 ? a.vt_col[mm] : a.row_pos[mm];
+  }
+  // bias of this lane's columns i*32 + 8g + 4hi + [0, 4)
+  uint2 braw[C::RN][4];
+#pragma unroll
+  for (int i = 0; i < C::RN; ++i)
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+      braw[i][g] = a.bias ? *reinterpret_cast<const uint2*>(a.bias + nq + i * 32 + 8 * g + 4 * hi)
+                          : make_uint2(0u, 0u);
+  auto bias = [&](int i, int v) {
+    const uint32_t w = (v & 2) ? braw[i][v >> 2].y : braw[i][v >> 2].x;
+    return bf2f((bf16_t)((v & 1) ? w >> 16 : w & 0xffffu));
+  };
+  if (region == 2) {
+    // V^T[n][vt_col[m]], 2 B per store; rows at or past M get an offset past the range
+    const __amdgpu_buffer_rsrc_t rv =
+        __builtin_amdgcn_make_buffer_rsrc((void*)a.vt, (short)0, 0x7fffffff, kBufferFlags);
+#pragma unroll
+    for (int k = 0; k < C::RM; ++k) {
+      const bool valid = m0 + wm * C::WTM + k * 32 + l32 < M;
+#pragma unroll
+      for (int i = 0; i < C::RN; ++i)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const uint32_t n = (uint32_t)(nq - 2 * H + i * 32 + 8 * (v >> 2) + 4 * hi + (v & 3));
+          const float y = (float)acc[i][k][v] + bias(i, v);
+          const uint32_t off = valid ? (n * (uint32_t)a.ld_vt + (uint32_t)rt[k]) * 2u : 0xffffffffu;
+          __builtin_amdgcn_raw_buffer_store_b16(f2bf(y), rv, off, 0, 0);
+        }
+    }
+    return 1;
+  }
+  // q / k rows of this tile: rows at or past M fall outside the range
+  const int rows = M - m0 < C::BM ? M - m0 : C::BM;
+  const __amdgpu_buffer_rsrc_t rc = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(a.C + (long)m0 * a.ldc), (short)0, (int)((uint32_t)rows * (uint32_t)a.ldc * 2u), kBufferFlags);
+  const bool rope = a.rope_cos && !(region == 0 && a.rope_q_in_attn);  // uniform
+  // RoPE factors of one row block: tables grouped by 32 positions (rope_table),
+  // this lane's d = 8g + 4hi + t
+  float4 cf[4], sf[4];
+  auto rope_load = [&](int pos) {
+    const long to = ((long)(pos >> 5) * 256 + (pos & 31) * 2 + hi) * 4;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      cf[g] = *reinterpret_cast<const float4*>(a.rope_cos + to + g * 256);
+      sf[g] = *reinterpret_cast<const float4*>(a.rope_sin + to + g * 256);
+    }
+  };
+  if (rope) rope_load(rt[0]);
+#pragma unroll
+  for (int k = 0; k < C::RM; ++k) {
+    const uint32_t rowoff = (uint32_t)(wm * C::WTM + k * 32 + l32) * (uint32_t)a.ldc;
+    uint2 out[C::RN >= 2 ? C::RN / 2 : 1][8];
+    // heads are pairs of 32-column blocks (i, i+1): d in [0,32) and [32,64)
+#pragma unroll
+    for (int i = 0; i < C::RN; i += 2) {
+      float x0[16], x1[16];
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        x0[v] = rbf((float)acc[i][k][v] + bias(i, v));
+        x1[v] = rbf((float)acc[i + 1][k][v] + bias(i + 1, v));
+      }
+      if (rope) {
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const float4 c4 = cf[v >> 2], s4 = sf[v >> 2];
+          const int t = v & 3;
+          const float c = t == 0 ? c4.x : t == 1 ? c4.y : t == 2 ? c4.z : c4.w;
+          const float sn = t == 0 ? s4.x : t == 1 ? s4.y : t == 2 ? s4.z : s4.w;
+          const float r0 = add_rn(mul_rn(x0[v], c), mul_rn(-x1[v], sn));
+          const float r1 = add_rn(mul_rn(x1[v], c), mul_rn(x0[v], sn));
+          x0[v] = r0;
+          x1[v] = r1;
+        }
+      }
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        out[i / 2][g] = pack4(x0[4 * g], x0[4 * g + 1], x0[4 * g + 2], x0[4 * g + 3]);
+        out[i / 2][4 + g] = pack4(x1[4 * g], x1[4 * g + 1], x1[4 * g + 2], x1[4 * g + 3]);
+      }
+    }
+    // the next block's factors go out before this block's stores
+    if (rope && k + 1 < C::RM) rope_load(rt[k + 1]);
+#pragma unroll
+    for (int i = 0; i < C::RN; i += 2)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const uint32_t col = (uint32_t)(nq + i * 32 + 8 * g + 4 * hi);
+        const u32x2 lo = {out[i / 2][g].x, out[i / 2][g].y}, hi2 = {out[i / 2][4 + g].x, out[i / 2][4 + g].y};
+        __builtin_amdgcn_raw_buffer_store_b64(lo, rc, (rowoff + col) * 2u, 0, 0);
+        __builtin_amdgcn_raw_buffer_store_b64(hi2, rc, (rowoff + col + 32u) * 2u, 0, 0);
+      }
+  }
+  return 0;
+}
+
 template <class C, int EPI, class ACC>
 __device__ __forceinline__ void run_epilogue(const GemmArgs& a, ACC (&acc)[C::RN][C::RM], int m0,
                                              int n0, int M, int wm, int wn, int l32, int hi) {
@@ -726,6 +847,9 @@ gemm_mfma_kernel(GemmArgs a) {
   // vmcnt holds at most 63: larger counts fall back to a full wait
   constexpr int kEpiStores = kWaitBase + kEpiStoresRaw < 64 ? kEpiStoresRaw : -1;
   constexpr int kStartWait = kWaitBase + (kEpiStores > 0 ? kEpiStores : 0);
+  // bf16 QKV on the single-issue schedules: qkv_epilogue_fixed, counted stores
+  constexpr bool kQkvFixed = base_epi(EPI) == EPI_QKV && !is_dq(EPI) && C::SCHED != 2 && C::RN % 2 == 0;
+  int qkv_kind = 2;  // the last QKV epilogue's stores: 0 q|k, 1 V (fixed counts), 2 unknown
   static_assert(kStartWait < 64, "vmcnt range");
   // one pipelined K step: k = step index, stage s = k % ST (compile-time)
   // one pipelined K step: k = step index within the item, stage s = k % ST (compile-time)
@@ -733,7 +857,14 @@ gemm_mfma_kernel(GemmArgs a) {
     constexpr int s = decltype(stc)::value;
     if (k >= KTi) return;  // uniform
     if (k == 0) {
-      if constexpr (kEpiStores >= 0 && ST == 2) {
+      if constexpr (kQkvFixed) {
+        // the QKV epilogue's fixed store counts; every older op (the prologue
+        // DMA of stage 0 first) is done once at most this many remain
+        constexpr int kQK = kWaitBase + C::RM * C::RN * 4, kV = kWaitBase + C::RM * C::RN * 16;
+        if (qkv_kind == 2 || (ST > 2 && KTi < ST - 1)) wait_vm_lgkm0<0>();
+        else if (qkv_kind == 0) wait_vm_lgkm0<(kQK < 63 ? kQK : 63)>();
+        else wait_vm_lgkm0<(kV < 63 ? kV : 63)>();
+      } else if constexpr (kEpiStores >= 0 && ST == 2) {
         wait_vm_lgkm0<kStartWait>();
       } else if constexpr (kEpiStores >= 0) {
         if (KTi >= ST - 1) wait_vm_lgkm0<(kEpiStores >= 0 ? kStartWait : 0)>();
@@ -965,6 +1096,8 @@ gemm_mfma_kernel(GemmArgs a) {
                                            : stB(std::integral_constant<int, fs>{})) +
                          (wave % (C::NW / 2)) * 32 * C::WTN;
       staged_epilogue<C, EPI>(a, acc, sop, rrows, m0, n0, M, wm, wn, lane, l32, hi, region);
+    } else if constexpr (kQkvFixed) {
+      qkv_kind = qkv_epilogue_fixed<C>(a, acc, m0, n0, M, wm, wn, l32, hi);
     } else {
       run_epilogue<C, EPI>(a, acc, m0, n0, M, wm, wn, l32, hi);
     }
