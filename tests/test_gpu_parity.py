@@ -142,6 +142,8 @@ VARIANTS = {
     "rope": R.DitConfig(**SMALL),
     "qknorm_bias": R.DitConfig(**SMALL, qkv_bias=True, qk_norm="LayerNorm"),
     "rms_norope": R.DitConfig(**SMALL, qk_norm="RMSNorm", rotary=False),
+    # q|k|v bias without qk-norm: the QKV epilogue with counted stores and its bias
+    "bias_rope": R.DitConfig(**SMALL, qkv_bias=True),
 }
 
 
