@@ -239,14 +239,14 @@ seq_attention_kernel(const uint16_t* __restrict__ qk, long ldqk, const uint16_t*
 #pragma unroll
   for (int c = 0; c < 4; ++c) vrd[c] = (uint32_t)att_off(l32, 2 * c + hi) * 2u;  // k-step (kb, half): c = 2kb + half
 
-  // masked: the tile crosses some lane's visible-key limit (wave-uniform test
-  // at the call site; two copies of the tile code, so unmasked tiles carry no
-  // per-score compare and select)
   // one 16-B fragment read per (lane address, block): the stage's base is added
   // once per address, the block offset rides in the instruction
   auto frag = [](uint32_t addr, int off) {
     return *reinterpret_cast<const __attribute__((address_space(3))) bf16x8*>((uintptr_t)(addr + off));
   };
+  // masked: the tile crosses some lane's visible-key limit (wave-uniform test
+  // at the call site; two copies of the tile code, so unmasked tiles carry no
+  // per-score compare and select)
   auto compute = [&](auto masked, const uint16_t* Ks, const uint16_t* Vs, int k0) {
     const uint32_t kst = (uint32_t)(uintptr_t)DFH_LPTR(Ks), vst = (uint32_t)(uintptr_t)DFH_LPTR(Vs);
     floatx16 s[2];

@@ -98,7 +98,7 @@ hipError_t ln_modulate(const uint16_t* x, long ldx, uint16_t* out, long ldo,
                        float* sx = nullptr);
 
 // One attention sequence (device array element). Rows index the q|k buffer
-// ([rows, 2H]: q in columns [0, H), k in [H, 2H)); V^T is [H, ld_vt].
+// ([rows, ldqk], ldqk >= 2H: q in columns [0, H), k in [H, 2H)); V^T is [H, ld_vt].
 struct AttnSeq {
   int q_row0;      // q|k row of query position 0
   int kv_row0;     // q|k row of key position 0
