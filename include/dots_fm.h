@@ -158,10 +158,12 @@ int dfh_input_status(DfhHandle* h, int* flags, void* stream);
  * 5 ln_modulate, 6 other, 7 the latent tail of the last block (see
  * dfh_set_latent_tail). */
 int dfh_profile_enable(DfhHandle* h, int enable);
-/* Which classes carry events while profiling is on: bit c for class c (default
- * all). Each timed launch adds a few microseconds of dispatch overhead, so a
- * timed region arms only the class it measures. */
-int dfh_profile_classes(DfhHandle* h, unsigned mask);
+/* Which launches carry events while profiling is on: of the classes in mask
+ * (bit c for class c; default all), launches 0, every, 2*every, ... of each
+ * class, counted from this call (default every = 1: all). An evented launch
+ * adds a few microseconds of dispatch before and after it, so a timed region
+ * arms a sample of the class it measures. every < 1 is an error. */
+int dfh_profile_classes(DfhHandle* h, unsigned mask, int every);
 /* K-split of each GEMM's last, partial round of tiles (default on): leftover
  * tiles are cut along K over the idle workgroups; the workgroup that completes a
  * tile adds the partial sums. Off: every tile runs whole. No reference counterpart

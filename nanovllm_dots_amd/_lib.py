@@ -112,7 +112,7 @@ SIGNATURES = {
     "dfh_profile_enable": (C.c_int, [vp, C.c_int]),
     "dfh_set_ksplit": (C.c_int, [vp, C.c_int]),
     "dfh_set_ln_quant": (C.c_int, [vp, C.c_int]),
-    "dfh_profile_classes": (C.c_int, [vp, C.c_uint]),
+    "dfh_profile_classes": (C.c_int, [vp, C.c_uint, C.c_int]),
     "dfh_set_latent_tail": (C.c_int, [vp, C.c_int]),
     "dfh_set_int8": (C.c_int, [vp, C.c_int, vp, vp]),
     "dfh_profile_read": (C.c_int, [vp, C.POINTER(C.c_double), C.POINTER(C.c_long), C.c_int]),

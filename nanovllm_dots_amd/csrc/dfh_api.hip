@@ -124,6 +124,8 @@ struct DfhHandle {
   // profiling
   bool prof = false;
   unsigned prof_mask = ~0u;  // classes whose launches carry events
+  int prof_every = 1;        // of those, every prof_every-th launch of its class
+  long prof_seen[PC_N] = {0};
   std::vector<hipEvent_t> ev_pool;
   std::vector<std::pair<int, int>> ev_used;  // (class, pool index of start)
   size_t ev_next = 0;
@@ -136,6 +138,7 @@ namespace {
 // arm dispatch-packet events for the next launch of class `pc`
 void prof_arm(DfhHandle* h, int pc) {
   if (!h->prof || !((h->prof_mask >> pc) & 1u)) return;
+  if (h->prof_seen[pc]++ % h->prof_every) return;
   if (h->ev_next + 2 > h->ev_pool.size()) return;  // pool full: drop the sample
   const int i = (int)h->ev_next;
   h->ev_next += 2;
@@ -967,9 +970,12 @@ int dfh_profile_enable(DfhHandle* h, int enable) {
   return 0;
 }
 
-int dfh_profile_classes(DfhHandle* h, unsigned mask) {
+int dfh_profile_classes(DfhHandle* h, unsigned mask, int every) {
   if (!h) return fail("null handle");
+  if (every < 1) return fail("every must be at least 1 (got %d)", every);
   h->prof_mask = mask;
+  h->prof_every = every;
+  for (auto& n : h->prof_seen) n = 0;
   return 0;
 }
 

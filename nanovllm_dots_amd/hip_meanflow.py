@@ -370,11 +370,12 @@ class HipFMHead:
         attention, O projection and MLP are computed there."""
         _lib.check(self.lib.dfh_set_latent_tail(self.handle, int(enable)), "dfh_set_latent_tail")
 
-    def profile(self, enable: bool, classes=None) -> None:
+    def profile(self, enable: bool, classes=None, every: int = 1) -> None:
         """Dispatch-packet events on the launches of ``classes`` (names from
-        PROFILE_CLASSES; None: all) while ``enable``; read with profile_read()."""
+        PROFILE_CLASSES; None: all) while ``enable``: launches 0, every,
+        2*every, ... of each class from this call on; read with profile_read()."""
         mask = 0xFFFFFFFF if classes is None else sum(1 << self.PROFILE_CLASSES.index(c) for c in classes)
-        _lib.check(self.lib.dfh_profile_classes(self.handle, mask), "dfh_profile_classes")
+        _lib.check(self.lib.dfh_profile_classes(self.handle, mask, int(every)), "dfh_profile_classes")
         _lib.check(self.lib.dfh_profile_enable(self.handle, int(enable)), "dfh_profile_enable")
 
     PROFILE_CLASSES = ("qkv_gemm", "o_gemm", "fc1_gemm", "fc2_gemm", "attention", "ln_modulate", "other",
