@@ -281,6 +281,39 @@ def test_noise_drawn_from_torch_rng_when_absent():
     assert torch.equal(a, b)
 
 
+def test_profile_class_mask_and_sample_stride():
+    """Dispatch events per class: with every = 1 each launch of every class
+    carries them; with a class mask and every = 3, launches 0, 3, 6, ... of
+    that class (counted across calls) and nothing else. The events do not
+    change the latents; every < 1 is an error."""
+    cfg = VARIANTS["rope"]  # 2 blocks: block 0 full rows, block 1 the latent tail
+    head, _ = _head(cfg, seed=5)
+    lens, hist, noise, inp, mask, pos, g = _inputs(cfg, 3, 20, 90, seed=5)
+    args = (_cuda_bf16(inp), pos.cuda(), _cuda_bf16(g), _cuda_bf16(noise), 4)
+    ref = head.solve(*args)
+    head.profile(True)
+    head.profile_read()
+    a = head.solve(*args)
+    torch.cuda.synchronize()
+    full = head.profile_read()
+    n_fc1 = full["fc1_gemm"][1]
+    print(f"profile: per-class launches {({k: v[1] for k, v in full.items()})}", flush=True)
+    assert n_fc1 == 4  # one full-row block per step
+    assert full["latent_tail"][1] > 0 and full["attention"][1] > 0
+    assert all(ms > 0 for ms, cnt in full.values() if cnt)
+    head.profile(True, classes=("fc1_gemm",), every=3)
+    b = head.solve(*args)
+    c = head.solve(*args)
+    torch.cuda.synchronize()
+    part = head.profile_read()
+    head.profile(False)
+    assert part["fc1_gemm"][1] == (2 * n_fc1 + 2) // 3  # launches 0, 3, 6 of the two solves' 8
+    assert all(cnt == 0 for k, (ms, cnt) in part.items() if k != "fc1_gemm")
+    assert torch.equal(a, ref) and torch.equal(b, ref) and torch.equal(c, ref)
+    with pytest.raises(RuntimeError, match="every"):
+        head.profile(True, classes=("fc1_gemm",), every=0)
+
+
 # ----------------------------------------------------------------------------- full size
 FULL = R.DitConfig(hidden=1024, heads=16, ffn=4096, n_blocks=12, latent_dim=64, patch=16)
 
