@@ -93,8 +93,8 @@ def host_cpu():
     return info
 
 
-def cpu_c1_block(threads: int, warmup: int = 3, runs: int = 10):
-    """C1 on the host: one DiT block (hidden 1024, 16 x 64 heads, MLP 4096) in
+def cpu_dit_block(threads: int, warmup: int = 3, runs: int = 10):
+    """One DiT block on the host (hidden 1024, 16 x 64 heads, MLP 4096) in
     float32 over 64 context + 16 latent rows, t = dt = 0.25, seed 0 (the oracle's
     DiTBlock, the computation tests/golden/c1_block.npz pins). Median of ``runs``
     timed runs after ``warmup``; GFLOP/s of the block's GEMMs (25,165,824 FLOP
@@ -393,7 +393,7 @@ def paged_bench(reps: int = 20):
 
 
 def varlen_bench(mf, hist, noise_d, g_d, ref_out, reps: int = 5):
-    """The same C3 solve from per-request history tensors (dfh_meanflow_solve_varlen):
+    """The same 64-request solve from per-request history tensors (dfh_meanflow_solve_varlen):
     no padded [N,T,H] batch, [N,T,T] mask or pos_ids exists."""
     import torch
     dev = noise_d.device
@@ -557,8 +557,8 @@ def main():
     if not args.no_cpu:
         host = host_cpu()
         log(f"host cpu: {host}")
-        c1 = cpu_c1_block(host["threads_used"])
-        log(f"cpu c1 block: {c1}")
+        c1 = cpu_dit_block(host["threads_used"])
+        log(f"cpu one-block fp32: {c1}")
         cpu = cpu_baseline(cfg, W, lens, hist, noise, args.cpu_budget, host["threads_used"])
 
     rec = {
@@ -594,7 +594,7 @@ def main():
         "cpu_baseline": ({k: (round(v, 5) if isinstance(v, float) else v) for k, v in cpu.items()
                           if k in ("value", "unit", "cores", "kind", "sample")} if cpu else None),
         "cpu_xRT": round(cpu["xRT"], 4) if cpu else None,
-        "cpu_c1_block_fp32": c1,
+        "cpu_dit_block_80rows_fp32": c1,
         "cpu_host": dict(host, torch=torch.__version__, mkldnn=torch.backends.mkldnn.is_available())
         if host else None,
     }

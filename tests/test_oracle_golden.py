@@ -76,7 +76,7 @@ def test_varlen_twin_equals_padded_reference(name):
         off += L + P
 
 
-def test_c1_block_matches_reference():
+def test_one_block_80_rows_matches_reference():
     g = load_golden("c1_block.npz")
     cfg = R.DitConfig(**ast.literal_eval(str(g["cfg"])))
     W = R.random_dit_weights(cfg, 0)
