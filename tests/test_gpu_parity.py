@@ -318,7 +318,7 @@ def test_profile_class_mask_and_sample_stride():
 FULL = R.DitConfig(hidden=1024, heads=16, ffn=4096, n_blocks=12, latent_dim=64, patch=16)
 
 
-def test_full_size_one_step_forward_c2():
+def test_full_size_one_step_forward_8_requests():
     """8 requests, contexts U{64..512} projected from 1536-d N(0,1) states, one
     DiT forward at t=0, dt=0.25 (12 blocks, H=1024)."""
     from nanovllm_dots_amd import HipDiT
@@ -332,13 +332,13 @@ def test_full_size_one_step_forward_c2():
     x[:, T - cfg.patch:] = zp
     t = torch.zeros(n)
     dt = torch.full((n,), 0.25)
-    print(f"c2 forward lens={lens}", flush=True)
+    print(f"8-request forward lens={lens}", flush=True)
     ref = R.dit_forward(Wb, cfg, x, t, dt, mask, pos, g, regime="bf16")[:, T - cfg.patch:]
     ref32 = R.dit_forward(Wb, cfg, x, t, dt, mask, pos, g, regime="fp32")[:, T - cfg.patch:]
     got = HipDiT(head=head)(x=_cuda_bf16(x), timesteps=t.cuda(), duration=dt.cuda(), pos_ids=pos.cuda(),
                             g_cond=_cuda_bf16(g))[:, T - cfg.patch:]
-    _assert_latents(got, ref, cfg.latent_dim, "c2-forward")
-    _assert_latents(got, ref32, cfg.latent_dim, "c2-forward vs fp32", cos_bar=FWD_FP32_COS)
+    _assert_latents(got, ref, cfg.latent_dim, "8-request forward")
+    _assert_latents(got, ref32, cfg.latent_dim, "8-request forward vs fp32", cos_bar=FWD_FP32_COS)
 
 
 def test_full_size_nfe4_solve():
